@@ -1,0 +1,278 @@
+"""Benchmark of the MI355X attention hot path (one JSON line on stdout).
+
+Headline workload (value): BASELINE configs[1] — Bonsai-4B decode attention
+over all 36 layers at ctx 4096, batch 1. One step = for each layer:
+q_norm_rope (1 token) -> kv_writeback of row 4096 -> split-K decode
+attention over 4097 rows, replayed from a HIP graph. Inputs are resident in
+HBM; the 36 layers' caches (350 MB per step) exceed the 256 MB Infinity
+Cache, so every step streams the KV cache from HBM.
+
+value = algorithmic bytes per step / step time, with per layer
+4097 rows x 2304 B (K+V: 2 x (128 qs + 4 x 4 B d)) + 16384 B (q in, out).
+
+Also reported: decode at ctx 32768 (config 5, rotating over 8 layers),
+prefill pp2048 (metric) and the 2048-on-2048 chunked prefill (config 4) in
+TFLOP/s of unmasked QK^T + PV work, and the CPU oracle on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "bonsai-pot_amd"))
+
+METRIC = "decode-attn HBM GB/s (%peak) ctx4K/32K; prefill-attn TFLOP/s (%MFMA) pp2048"
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+KV_ROW_BYTES = 2 * 8 * (128 + 16)   # 2304 B per cache row: K + V, 8 KV heads, 128 qs + 4 f32 d
+QO_BYTES = 2 * 32 * 128 * 2         # q in + out, f16
+
+
+def decode_bytes(n_keys: int) -> int:
+    return n_keys * KV_ROW_BYTES + QO_BYTES
+
+
+def prefill_flops(m: int, pos: int, n_head=32, d=128) -> int:
+    pairs = m * pos + m * (m + 1) // 2      # unmasked (query, key) pairs per head
+    return 4 * d * n_head * pairs
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "prefill", "chunked"], default=None,
+                    help="run only one workload (for profiling)")
+    return ap.parse_args()
+
+
+class Bench:
+    def __init__(self, torch, n_layer, max_seq, m_tokens, seed=0):
+        from bonsai_pot_amd import Model, layout
+        self.torch = torch
+        self.cfg = layout.Config(n_layer=n_layer)
+        cfg = self.cfg
+        self.model = Model(cfg, max_seq)
+        self.stream = torch.cuda.current_stream()
+        self.model.set_stream(self.stream.cuda_stream)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.m = m_tokens
+        # act: q [m, 4096] | k_cur [m, 1024] | v_cur [m, 1024] | out [m, 4096]
+        self.q_off = 0
+        self.k_off = m_tokens * cfg.q_dim
+        self.v_off = self.k_off + m_tokens * cfg.kv_dim
+        self.out_off = self.v_off + m_tokens * cfg.kv_dim
+        n = self.out_off + m_tokens * cfg.q_dim
+        self.act = torch.randn(n, generator=g, device="cuda", dtype=torch.float32).to(torch.float16)
+        self.w = torch.ones(2 * cfg.head_dim, device="cuda", dtype=torch.float16)
+        self.a, self.wp = self.act.data_ptr(), self.w.data_ptr()
+
+    def fill_cache(self, rows: int, layers=None, seed=1):
+        """Writes cache rows [0, rows) of each layer with kv_writeback of random K/V."""
+        torch = self.torch
+        cfg = self.cfg
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        chunk = 4096
+        buf = torch.empty(2 * chunk * cfg.kv_dim, device="cuda", dtype=torch.float16)
+        for il in (range(cfg.n_layer) if layers is None else layers):
+            for r0 in range(0, rows, chunk):
+                n = min(chunk, rows - r0)
+                buf.copy_(torch.randn(buf.numel(), generator=g, device="cuda").to(torch.float16))
+                self.model.dispatch_kv_writeback_fused(buf.data_ptr(), self.wp, 0, chunk * cfg.kv_dim,
+                                                       cfg.head_dim, il, r0, n)
+        torch.cuda.synchronize()
+
+
+def time_region(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def per_launch_us(torch, launch, n_launch):
+    """Average device duration of single launches, each bracketed by HIP events
+    on the stream the kernel runs on."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_launch)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_launch)]
+    for i in range(n_launch):
+        starts[i].record()
+        launch(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    ts = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))
+    return sum(ts) / len(ts), ts[len(ts) // 2]
+
+
+def run_decode_step(b: "Bench", pos: int, layers):
+    m = b.model
+    for il in layers:
+        m.dispatch_q_norm_rope_fused(b.a, b.wp, b.q_off, 0, pos, 1)
+        m.dispatch_kv_writeback_fused(b.a, b.wp, b.k_off, b.v_off, 128, il, pos, 1)
+        m.dispatch_attention_decode(b.a, b.q_off, b.out_off, il, pos)
+
+
+def make_graph(torch, b, body):
+    """Captures body() (launches on b.model's stream) into a HIP graph."""
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        b.model.set_stream(side.cuda_stream)
+        body()                                   # warm-up outside capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            body()
+    b.model.set_stream(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return graph
+
+
+def bench_decode(torch, args, ctx, n_layer, graph_ok=True):
+    pos = ctx                                    # step at pos attends pos + 1 rows
+    b = Bench(torch, n_layer, pos + 1 + 63, 1, seed=ctx)
+    b.fill_cache(pos, seed=ctx + 1)
+    layers = list(range(n_layer))
+    step_bytes = n_layer * decode_bytes(pos + 1)
+    body = lambda: run_decode_step(b, pos, layers)
+    eager_s = time_region(torch, body, max(3, args.steps // 5), 2)
+    graph_s = None
+    if graph_ok and not args.no_graph:
+        g = make_graph(torch, b, body)
+        graph_s = time_region(torch, g.replay, args.steps, args.warmup)
+    step_s = graph_s if graph_s is not None else eager_s
+    # dominant kernel: decode attention alone, per launch, rotating layers
+    n_l = 4 * n_layer
+    avg_us, med_us = per_launch_us(
+        torch, lambda i: b.model.dispatch_attention_decode(b.a, b.q_off, b.out_off, i % n_layer, pos), n_l)
+    kbytes = decode_bytes(pos + 1)
+    res = {
+        "ctx": ctx, "n_keys": pos + 1, "layers": n_layer,
+        "ms_per_step": step_s * 1e3, "ms_per_step_eager": eager_s * 1e3,
+        "ms_per_step_graph": None if graph_s is None else graph_s * 1e3,
+        "step_GBps": step_bytes / step_s / 1e9,
+        "kernel_us_avg": avg_us, "kernel_us_median": med_us,
+        "kernel_bytes": kbytes, "kernel_GBps": kbytes / (avg_us * 1e-6) / 1e9,
+    }
+    res["kernel_frac_hbm"] = res["kernel_GBps"] / HBM_PEAK_GBS
+    b.model.close()
+    return res, step_bytes
+
+
+def bench_prefill(torch, args, m, pos):
+    n_layer = 2
+    b = Bench(torch, n_layer, pos + m, m, seed=m + pos)
+    b.fill_cache(pos + m, seed=3)
+    flops = prefill_flops(m, pos)
+    n = max(6, args.steps // 5)
+    for i in range(3):
+        b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True)
+    torch.cuda.synchronize()
+    avg_us, med_us = per_launch_us(
+        torch, lambda i: b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True), n)
+    tflops = flops / (avg_us * 1e-6) / 1e12
+    b.model.close()
+    return {"m_tokens": m, "pos_base": pos, "flops": flops, "kernel_us_avg": avg_us,
+            "kernel_us_median": med_us, "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS}
+
+
+def cpu_baseline(seconds=10.0):
+    """CPU oracle (scalar C restatement of the reference's split/merge decode),
+    1 thread, decode at ctx 4096 over as many layers as fit in ~seconds."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    from bonsai_pot_amd import layout
+    n_keys, max_seq, n_layer = 4097, 4097, 4
+    nbytes = layout.kv_buffer_bytes(n_layer, 1024, max_seq)
+    rng = np.random.default_rng(0)
+    kv = []
+    for _ in range(2):
+        buf = rng.integers(-127, 128, nbytes, dtype=np.int8).view(np.uint8)
+        nd = n_layer * max_seq * 32
+        buf[:nd * 4].view(np.float32)[:] = np.float32(0.02)
+        kv.append(buf)
+    act = rng.standard_normal(2 * 4096).astype(np.float16).view(np.uint16)
+    layers = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        il = layers % n_layer
+        d_word, qs_byte = layout.kv_layer_offsets(n_layer, 1024, max_seq, il)
+        p = orc.AttnSplitParams(head_dim=128, n_head=32, n_kv_head=8, pos=n_keys, kv_stride=1024,
+                                q_offset=0, k_d_word_offset=d_word, k_qs_byte_offset=qs_byte,
+                                v_d_word_offset=d_word, v_qs_byte_offset=qs_byte,
+                                n_chunks_active=(n_keys + 15) // 16, scale=128 ** -0.5,
+                                out_offset=4096)
+        orc.attention_split_merge(p, act, kv[0], kv[1])
+        layers += 1
+    dt = time.perf_counter() - t0
+    return {"value": decode_bytes(n_keys) * layers / dt / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{layers} layer-decodes at ctx 4096 (4097 rows, 32 q heads) in {dt:.1f} s, "
+                      "scalar C oracle restating attention_split + attention_merge"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported (this build "
+              "measures one MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    torch.cuda.init()
+    extras = {}
+    if args.only in (None, "decode4k"):
+        d4, step_bytes = bench_decode(torch, args, 4096, 36)
+        extras["decode_ctx4096_36layers"] = d4
+    if args.only in (None, "decode32k"):
+        d32, _ = bench_decode(torch, args, 32768, 8)
+        extras["decode_ctx32768"] = d32
+    if args.only in (None, "prefill"):
+        extras["prefill_pp2048"] = bench_prefill(torch, args, 2048, 0)
+        extras["prefill_pp512"] = bench_prefill(torch, args, 512, 0)
+    if args.only in (None, "chunked"):
+        extras["chunked_prefill_2048_on_2048"] = bench_prefill(torch, args, 2048, 2048)
+    if args.only is not None:
+        print(json.dumps(extras), flush=True)
+        return
+    cpu = None if args.skip_cpu else cpu_baseline()
+    out = {
+        "metric": METRIC,
+        "value": d4["step_GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": d4["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (i8 Q8_0 cache, f16 q/out)",
+        "data": "synthetic (seeded N(0,1) q/k/v through kv_writeback; no model weights)",
+        "config": {"workload": "configs[1]: Bonsai-4B decode attention, 36 layers, ctx 4096, batch 1 "
+                               "(q_norm_rope + kv_writeback + split-K decode per layer, HIP graph)",
+                   "n_head": 32, "n_kv_head": 8, "head_dim": 128, "ctx": 4096, "layers": 36,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": d4["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": d4["kernel_frac_hbm"], "traffic": None,
+                     "kernel": "decode_kernel", "bytes_per_launch": d4["kernel_bytes"],
+                     "us_per_launch": d4["kernel_us_avg"]},
+        "cpu_baseline": cpu,
+        **extras,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

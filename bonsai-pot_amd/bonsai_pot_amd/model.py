@@ -1,0 +1,183 @@
+"""ctypes binding of ``libbonsai_pot_hip.so`` and the :class:`Model` wrapper.
+
+:class:`Model` mirrors the attention part of the reference's ``Model``
+(src/model.rs) and the dispatch helpers of src/forward.rs, one method per
+C entry point; every failing status raises the matching :class:`PotError`.
+"""
+import ctypes
+import os
+
+from .errors import BP_OK, error_for
+from .layout import Config
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+library_path = os.path.join(os.path.dirname(_HERE), "lib", "libbonsai_pot_hip.so")
+
+if not os.path.exists(library_path):
+    raise ImportError(
+        f"{library_path} is missing: build the HIP library first "
+        "(python bonsai-pot_amd/build.py or __graft_entry__.build()); there is no CPU fallback")
+
+
+
+def _preload_torch_hip_runtime() -> None:
+    """One HIP runtime per process. PyTorch-ROCm wheels bundle their own
+    libamdhip64 (soname libamdhip64.so.7) and load it by file name; if this
+    library were loaded first it would bring in /opt/rocm's copy and the process
+    would hold two runtimes (separate device/stream state). Loading torch's copy
+    first, RTLD_GLOBAL, makes both resolve to the same runtime. Nothing is
+    imported from torch."""
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return
+    for loc in spec.submodule_search_locations:
+        cand = os.path.join(loc, "lib", "libamdhip64.so")
+        if os.path.exists(cand):
+            ctypes.CDLL(cand, mode=ctypes.RTLD_GLOBAL)
+            return
+
+
+_preload_torch_hip_runtime()
+lib = ctypes.CDLL(library_path)
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [("n_layer", ctypes.c_uint32), ("n_head", ctypes.c_uint32),
+                ("n_kv_head", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+                ("rms_eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float)]
+
+
+_u32, _u64, _vp, _i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int32
+_SIGS = {
+    "bp_model_create": (_i32, [ctypes.POINTER(_Config), _u32, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "bp_model_destroy": (None, [_vp]),
+    "bp_model_set_stream": (_i32, [_vp, _vp]),
+    "bp_model_synchronize": (_i32, [_vp]),
+    "bp_model_kv_buffers": (_i32, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_u64)]),
+    "bp_model_rope_table": (_i32, [_vp, ctypes.POINTER(_vp)]),
+    "bp_model_max_seq": (_u32, [_vp]),
+    "bp_kv_layer_offsets": (_i32, [_u32, _u32, _u32, _u32, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "bp_kv_buffer_bytes": (_u64, [_u32, _u32, _u32]),
+    "bp_dispatch_q_norm_rope_fused": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_kv_writeback_fused": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_attention_decode": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_attention": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "bp_kv_snapshot_payload_bytes": (_u64, [_u32, _u32, _u32]),
+    "bp_kv_snapshot_capture": (_i32, [_vp, _u32, _vp, _u64]),
+    "bp_kv_snapshot_apply": (_i32, [_vp, _u32, _vp, _u64]),
+    "bp_check_device": (_i32, [_vp]),
+    "bp_debug_lose_device": (_i32, [_vp]),
+    "bp_last_error": (ctypes.c_char_p, []),
+    "bp_status_name": (ctypes.c_char_p, [_i32]),
+}
+EXPORTED_SYMBOLS = tuple(_SIGS)
+for _name, (_res, _args) in _SIGS.items():
+    _fn = getattr(lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def _check(status: int) -> None:
+    if status != BP_OK:
+        msg = lib.bp_last_error().decode(errors="replace")
+        name = lib.bp_status_name(status).decode()
+        raise error_for(status, f"{name}: {msg}")
+
+
+class Model:
+    """Device-side state of the attention path for one model on one GPU."""
+
+    def __init__(self, cfg: Config, max_seq: int, device: int = 0):
+        self.cfg = cfg
+        self.max_seq = max_seq
+        c = _Config(cfg.n_layer, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.rms_eps,
+                    cfg.rope_freq_base)
+        h = _vp()
+        _check(lib.bp_model_create(ctypes.byref(c), max_seq, device, ctypes.byref(h)))
+        self._h = h
+
+    # -- lifetime ------------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib.bp_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    # -- buffers ---------------------------------------------------------------
+    def set_stream(self, stream_ptr: int) -> None:
+        _check(lib.bp_model_set_stream(self._h, stream_ptr))
+
+    def synchronize(self) -> None:
+        _check(lib.bp_model_synchronize(self._h))
+
+    def kv_buffers(self):
+        """(kv_k device address, kv_v device address, bytes of each)."""
+        k, v, n = _vp(), _vp(), _u64()
+        _check(lib.bp_model_kv_buffers(self._h, ctypes.byref(k), ctypes.byref(v), ctypes.byref(n)))
+        return k.value, v.value, n.value
+
+    def rope_table(self) -> int:
+        p = _vp()
+        _check(lib.bp_model_rope_table(self._h, ctypes.byref(p)))
+        return p.value
+
+    def layer_offsets(self, il: int):
+        d, q = _u64(), _u64()
+        _check(lib.bp_kv_layer_offsets(self.cfg.n_layer, self.cfg.kv_dim, self.max_seq, il,
+                                       ctypes.byref(d), ctypes.byref(q)))
+        return d.value, q.value
+
+    # -- dispatch helpers (src/forward.rs) -------------------------------------
+    def dispatch_q_norm_rope_fused(self, act: int, w_norms: int, q_off: int, w_q_norm_off: int,
+                                   pos_base: int, m_tokens: int) -> None:
+        _check(lib.bp_dispatch_q_norm_rope_fused(self._h, act, w_norms, q_off, w_q_norm_off,
+                                                 pos_base, m_tokens))
+
+    def dispatch_kv_writeback_fused(self, act: int, w_norms: int, k_cur_off: int, v_cur_off: int,
+                                    w_k_norm_off: int, layer_il: int, pos_base: int,
+                                    m_tokens: int) -> None:
+        _check(lib.bp_dispatch_kv_writeback_fused(self._h, act, w_norms, k_cur_off, v_cur_off,
+                                                  w_k_norm_off, layer_il, pos_base, m_tokens))
+
+    def dispatch_attention_decode(self, act: int, q_off: int, out_off: int, layer_il: int,
+                                  pos: int) -> None:
+        _check(lib.bp_dispatch_attention_decode(self._h, act, q_off, out_off, layer_il, pos))
+
+    def dispatch_attention(self, act: int, q_off: int, out_off: int, layer_il: int, pos: int,
+                           m_tokens: int, is_prefill: bool) -> None:
+        _check(lib.bp_dispatch_attention(self._h, act, q_off, out_off, layer_il, pos, m_tokens,
+                                         1 if is_prefill else 0))
+
+    # -- snapshot payload (src/kv_snapshot.rs:203-372) ----------------------------
+    def snapshot_payload(self, pos: int) -> bytes:
+        n = lib.bp_kv_snapshot_payload_bytes(self.cfg.n_layer, self.cfg.kv_dim, pos)
+        buf = ctypes.create_string_buffer(max(n, 1))
+        _check(lib.bp_kv_snapshot_capture(self._h, pos, buf, n))
+        return buf.raw[:n]
+
+    def apply_payload(self, pos: int, payload: bytes) -> None:
+        buf = ctypes.create_string_buffer(bytes(payload), max(len(payload), 1))
+        _check(lib.bp_kv_snapshot_apply(self._h, pos, buf, len(payload)))
+
+    # -- device loss (src/model.rs:1733-1751) -----------------------------------
+    def check_device(self) -> None:
+        _check(lib.bp_check_device(self._h))
+
+    def is_device_lost(self) -> bool:
+        return lib.bp_check_device(self._h) != BP_OK
+
+    def _destroy_device_for_test(self) -> None:
+        _check(lib.bp_debug_lose_device(self._h))

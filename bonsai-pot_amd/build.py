@@ -1,0 +1,51 @@
+"""Build recipe for the gfx950 shared library libbonsai_pot_hip.so (in-tree).
+
+Every source under csrc/ is compiled by hipcc for gfx950 only, with
+-ffp-contract=off (the norm/RoPE/quantize stages are bit-exact by construction
+and must not be fused into FMAs behind their back) and with packed-FP32 ops
+disabled for device code.
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "lib", "libbonsai_pot_hip.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+SOURCES = ["bp_api.cpp", "norm_rope_writeback.hip", "attn_decode.hip", "attn_prefill.hip"]
+FLAGS = [
+    "-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+    "-ffp-contract=off", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
+        raise RuntimeError(f"hipcc failed ({r.returncode}) on {cmd[-1]}")
+    return r
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every kernel and the host layer, link the shared library, return its path."""
+    obj_dir = os.path.join(HERE, "lib", "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    jobs = []
+    for src in SOURCES:
+        obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
+        jobs.append((obj, [HIPCC, *FLAGS, "-c", "-o", obj, os.path.join(CSRC, src)]))
+    with ThreadPoolExecutor(max_workers=min(4, len(jobs))) as ex:
+        list(ex.map(lambda j: _run(j[1]), jobs))
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB, *[o for o, _ in jobs]])
+    if verbose:
+        print("built", LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)

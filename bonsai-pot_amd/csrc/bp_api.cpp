@@ -1,0 +1,464 @@
+// Host layer of the MI355X attention path: the C ABI declared in
+// include/bonsai_pot_hip.h.
+//
+// It restates, for HIP, the parts of the reference's host code (paths relative
+// to the reference repository root) that the attention path needs:
+//   - Model::load_with_options, KV / RoPE / partials part (src/model.rs:1148-1248):
+//     bp_model_create, with the same config validation (head_dim == 128,
+//     kv_dim % 32 == 0) and the same KV byte layout;
+//   - the dispatch helpers of src/forward.rs (:48-58, :359-413, :501-532,
+//     :820-857): bp_kv_layer_offsets and bp_dispatch_*;
+//   - kv_snapshot::capture / apply (src/kv_snapshot.rs:203-372);
+//   - the device-loss latch (src/model.rs:1087-1098, :1733-1751).
+// Kernels never allocate: everything a launch touches is created here once.
+#include "../../include/bonsai_pot_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "bp_kernels.hpp"
+
+struct bp_model {
+    bp_config cfg;
+    uint32_t kv_dim, q_dim, nb_per_row, max_seq;
+    int device;
+    int cu_count;
+    hipStream_t stream;
+    uint8_t* kv_k;
+    uint8_t* kv_v;
+    uint64_t kv_bytes;
+    uint16_t* rope_cs;
+    float* partials;
+    uint64_t partials_floats;
+    uint32_t* tickets;
+    bool lost;
+    std::string lost_message;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+bp_status fail(bp_status code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+// Errors after which the context (and every later call) is unusable.
+bool is_device_fatal(hipError_t e) {
+    switch (e) {
+        case hipErrorIllegalAddress:
+        case hipErrorLaunchFailure:
+        case hipErrorLaunchTimeOut:
+        case hipErrorECCNotCorrectable:
+        case hipErrorAssert:
+        case hipErrorContextIsDestroyed:
+            return true;
+        default:
+            return false;
+    }
+}
+
+bp_status hip_check(bp_model* m, hipError_t e, const char* what) {
+    if (e == hipSuccess) return BP_OK;
+    if (m && is_device_fatal(e)) {
+        m->lost = true;
+        m->lost_message = std::string(what) + ": " + hipGetErrorString(e);
+        return fail(BP_ERR_DEVICE_LOST, "device lost: %s", m->lost_message.c_str());
+    }
+    return fail(BP_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bp_status check_model(const bp_model* m) {
+    if (!m) return fail(BP_ERR_INVALID_ARG, "model is NULL");
+    if (m->lost) return fail(BP_ERR_DEVICE_LOST, "device lost: %s", m->lost_message.c_str());
+    return BP_OK;
+}
+
+// Makes the model's device current for this thread.
+bp_status enter(bp_model* m) {
+    bp_status st = check_model(m);
+    if (st != BP_OK) return st;
+    return hip_check(m, hipSetDevice(m->device), "hipSetDevice");
+}
+
+// half::f16::from_f32 semantics (round to nearest even), for the RoPE table.
+uint16_t host_f32_to_f16(float v) {
+    _Float16 h = static_cast<_Float16>(v);
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+
+// src/model.rs:1756-1769: theta_j = base^(-2j/head_dim) in f64, (cos, sin)
+// of p*theta_j in f64 -> f32, interleaved per j; uploaded as f16 (:1149).
+std::vector<uint16_t> build_rope_table(const bp_config& cfg, uint32_t max_seq) {
+    const uint32_t hd = cfg.head_dim, half = hd / 2;
+    std::vector<uint16_t> out(static_cast<size_t>(max_seq) * hd);
+    std::vector<double> theta(half);
+    for (uint32_t j = 0; j < half; j++)
+        theta[j] = std::pow(static_cast<double>(cfg.rope_freq_base),
+                            -2.0 * static_cast<double>(j) / static_cast<double>(hd));
+    for (uint32_t p = 0; p < max_seq; p++) {
+        for (uint32_t j = 0; j < half; j++) {
+            const double angle = static_cast<double>(p) * theta[j];
+            out[static_cast<size_t>(p) * hd + 2 * j] = host_f32_to_f16(static_cast<float>(std::cos(angle)));
+            out[static_cast<size_t>(p) * hd + 2 * j + 1] = host_f32_to_f16(static_cast<float>(std::sin(angle)));
+        }
+    }
+    return out;
+}
+
+uint64_t kv_d_word(const bp_model* m, uint32_t il) {
+    return static_cast<uint64_t>(il) * m->max_seq * m->nb_per_row;
+}
+uint64_t kv_qs_byte(const bp_model* m, uint32_t il) {
+    return static_cast<uint64_t>(m->cfg.n_layer) * m->max_seq * m->nb_per_row * 4 +
+           static_cast<uint64_t>(il) * m->max_seq * m->kv_dim;
+}
+bp::KvView kv_view(const bp_model* m, const uint8_t* buf, uint32_t il) {
+    bp::KvView v;
+    v.d = reinterpret_cast<const float*>(buf) + kv_d_word(m, il);
+    v.qs = reinterpret_cast<const int8_t*>(buf + kv_qs_byte(m, il));
+    return v;
+}
+
+constexpr uint32_t kMaxGridY = 65535;
+
+}  // namespace
+
+extern "C" {
+
+const char* bp_last_error(void) { return g_last_error.c_str(); }
+
+const char* bp_status_name(bp_status s) {
+    switch (s) {
+        case BP_OK: return "BP_OK";
+        case BP_ERR_CONFIG: return "BP_ERR_CONFIG";
+        case BP_ERR_CONTEXT_OVERFLOW: return "BP_ERR_CONTEXT_OVERFLOW";
+        case BP_ERR_INVALID_ARG: return "BP_ERR_INVALID_ARG";
+        case BP_ERR_HIP: return "BP_ERR_HIP";
+        case BP_ERR_DEVICE_LOST: return "BP_ERR_DEVICE_LOST";
+        case BP_ERR_OUT_OF_MEMORY: return "BP_ERR_OUT_OF_MEMORY";
+        case BP_ERR_NO_DEVICE: return "BP_ERR_NO_DEVICE";
+        default: return "BP_ERR_UNKNOWN";
+    }
+}
+
+uint64_t bp_kv_buffer_bytes(uint32_t n_layer, uint32_t kv_dim, uint32_t max_seq) {
+    const uint64_t rows = static_cast<uint64_t>(n_layer) * max_seq;
+    return rows * (kv_dim / 32) * 4 + rows * kv_dim;
+}
+
+bp_status bp_kv_layer_offsets(uint32_t n_layer, uint32_t kv_dim, uint32_t max_seq, uint32_t il,
+                              uint64_t* d_word_offset, uint64_t* qs_byte_offset) {
+    if (il >= n_layer) return fail(BP_ERR_INVALID_ARG, "layer %u >= n_layer %u", il, n_layer);
+    if (kv_dim % 32 != 0) return fail(BP_ERR_CONFIG, "kv_dim must be a multiple of 32 (Q8_0 block size)");
+    const uint64_t nb = kv_dim / 32;
+    if (d_word_offset) *d_word_offset = static_cast<uint64_t>(il) * max_seq * nb;
+    if (qs_byte_offset)
+        *qs_byte_offset = static_cast<uint64_t>(n_layer) * max_seq * nb * 4 +
+                          static_cast<uint64_t>(il) * max_seq * kv_dim;
+    return BP_OK;
+}
+
+uint64_t bp_kv_snapshot_payload_bytes(uint32_t n_layer, uint32_t kv_dim, uint32_t pos) {
+    const uint64_t d_layer = static_cast<uint64_t>(pos) * (kv_dim / 32) * 4;
+    const uint64_t qs_layer = static_cast<uint64_t>(pos) * kv_dim;
+    return 2ull * n_layer * (d_layer + qs_layer);
+}
+
+bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp_model** out) {
+    if (!cfg || !out) return fail(BP_ERR_INVALID_ARG, "cfg/out is NULL");
+    *out = nullptr;
+    // Validation mirrors src/model.rs:1174-1183 plus the kernels' fixed shapes.
+    if (cfg->head_dim != bp::kHeadDim)
+        return fail(BP_ERR_CONFIG, "head_dim must be 128 (got %u)", cfg->head_dim);
+    if (cfg->n_kv_head == 0 || cfg->n_head != cfg->n_kv_head * bp::kGroup)
+        return fail(BP_ERR_CONFIG, "n_head must be 4 * n_kv_head (got %u, %u)", cfg->n_head,
+                    cfg->n_kv_head);
+    if (cfg->n_layer == 0) return fail(BP_ERR_CONFIG, "n_layer must be > 0");
+    if (max_seq == 0) return fail(BP_ERR_CONFIG, "max_seq must be > 0");
+    if (!(cfg->rms_eps >= 0.0f) || !(cfg->rope_freq_base > 0.0f))
+        return fail(BP_ERR_CONFIG, "rms_eps must be >= 0 and rope_freq_base > 0");
+    int n_dev = 0;
+    if (hipGetDeviceCount(&n_dev) != hipSuccess || n_dev == 0)
+        return fail(BP_ERR_NO_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n_dev)
+        return fail(BP_ERR_INVALID_ARG, "device %d out of range (%d devices)", device, n_dev);
+
+    bp_model* m = new bp_model();
+    m->cfg = *cfg;
+    m->kv_dim = cfg->n_kv_head * cfg->head_dim;
+    m->q_dim = cfg->n_head * cfg->head_dim;
+    m->nb_per_row = m->kv_dim / 32;
+    m->max_seq = max_seq;
+    m->device = device;
+    m->stream = nullptr;
+    m->lost = false;
+    bp_status st = BP_OK;
+    auto bail = [&](bp_status s) { bp_model_destroy(m); return s; };
+    if ((st = hip_check(nullptr, hipSetDevice(device), "hipSetDevice")) != BP_OK) return bail(st);
+    hipDeviceProp_t prop;
+    if ((st = hip_check(nullptr, hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties")) != BP_OK)
+        return bail(st);
+    m->cu_count = prop.multiProcessorCount;
+
+    m->kv_bytes = bp_kv_buffer_bytes(cfg->n_layer, m->kv_dim, max_seq);
+    // Split-K partials: at most ~2 workgroups per CU -> bounded split count;
+    // size for the worst case of the planner over [1, max_seq] rows.
+    uint32_t split_len = 0, n_splits = 0;
+    bp::decode_plan(max_seq, cfg->n_kv_head, m->cu_count, &split_len, &n_splits);
+    const uint64_t max_splits = static_cast<uint64_t>(2 * m->cu_count / cfg->n_kv_head + 2);
+    m->partials_floats = static_cast<uint64_t>(cfg->n_head) * std::max<uint64_t>(max_splits, n_splits) *
+                         (bp::kHeadDim + 2);
+    const size_t rope_elems = static_cast<size_t>(max_seq) * cfg->head_dim;
+    if (hipMalloc(&m->kv_k, m->kv_bytes) != hipSuccess || hipMalloc(&m->kv_v, m->kv_bytes) != hipSuccess ||
+        hipMalloc(&m->rope_cs, rope_elems * 2) != hipSuccess ||
+        hipMalloc(&m->partials, m->partials_floats * 4) != hipSuccess ||
+        hipMalloc(&m->tickets, cfg->n_kv_head * sizeof(uint32_t)) != hipSuccess) {
+        (void)hipGetLastError();
+        return bail(fail(BP_ERR_OUT_OF_MEMORY, "hipMalloc failed for KV cache of %llu bytes x2",
+                         static_cast<unsigned long long>(m->kv_bytes)));
+    }
+    std::vector<uint16_t> rope = build_rope_table(*cfg, max_seq);
+    if ((st = hip_check(m, hipMemcpy(m->rope_cs, rope.data(), rope_elems * 2, hipMemcpyHostToDevice),
+                        "upload rope table")) != BP_OK ||
+        (st = hip_check(m, hipMemset(m->kv_k, 0, m->kv_bytes), "zero kv_k")) != BP_OK ||
+        (st = hip_check(m, hipMemset(m->kv_v, 0, m->kv_bytes), "zero kv_v")) != BP_OK ||
+        (st = hip_check(m, hipMemset(m->tickets, 0, cfg->n_kv_head * sizeof(uint32_t)), "zero tickets")) != BP_OK ||
+        (st = hip_check(m, hipDeviceSynchronize(), "model create sync")) != BP_OK)
+        return bail(st);
+    *out = m;
+    return BP_OK;
+}
+
+void bp_model_destroy(bp_model* m) {
+    if (!m) return;
+    if (hipSetDevice(m->device) == hipSuccess) {
+        if (!m->lost && m->stream) (void)hipStreamSynchronize(m->stream);
+        if (m->kv_k) (void)hipFree(m->kv_k);
+        if (m->kv_v) (void)hipFree(m->kv_v);
+        if (m->rope_cs) (void)hipFree(m->rope_cs);
+        if (m->partials) (void)hipFree(m->partials);
+        if (m->tickets) (void)hipFree(m->tickets);
+    }
+    (void)hipGetLastError();
+    delete m;
+}
+
+bp_status bp_model_set_stream(bp_model* m, void* stream) {
+    bp_status st = check_model(m);
+    if (st != BP_OK) return st;
+    m->stream = static_cast<hipStream_t>(stream);
+    return BP_OK;
+}
+
+bp_status bp_model_synchronize(bp_model* m) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    return hip_check(m, hipStreamSynchronize(m->stream), "hipStreamSynchronize");
+}
+
+bp_status bp_model_kv_buffers(const bp_model* m, void** kv_k, void** kv_v, uint64_t* bytes_each) {
+    if (!m) return fail(BP_ERR_INVALID_ARG, "model is NULL");
+    if (kv_k) *kv_k = m->kv_k;
+    if (kv_v) *kv_v = m->kv_v;
+    if (bytes_each) *bytes_each = m->kv_bytes;
+    return BP_OK;
+}
+
+bp_status bp_model_rope_table(const bp_model* m, const void** rope_cs) {
+    if (!m || !rope_cs) return fail(BP_ERR_INVALID_ARG, "model/rope_cs is NULL");
+    *rope_cs = m->rope_cs;
+    return BP_OK;
+}
+
+uint32_t bp_model_max_seq(const bp_model* m) { return m ? m->max_seq : 0; }
+
+bp_status bp_check_device(const bp_model* m) { return check_model(m); }
+
+bp_status bp_debug_lose_device(bp_model* m) {
+    if (!m) return fail(BP_ERR_INVALID_ARG, "model is NULL");
+    m->lost = true;
+    m->lost_message = "device destroyed by bp_debug_lose_device";
+    return BP_OK;
+}
+
+bp_status bp_dispatch_q_norm_rope_fused(bp_model* m, void* act, const void* w_norms, uint32_t q_off,
+                                        uint32_t w_q_norm_off, uint32_t pos_base, uint32_t m_tokens) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act || !w_norms) return fail(BP_ERR_INVALID_ARG, "act/w_norms is NULL");
+    if (m_tokens == 0) return BP_OK;
+    if (static_cast<uint64_t>(pos_base) + m_tokens > m->max_seq)
+        return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens %u > max_seq %u",
+                    pos_base, m_tokens, m->max_seq);
+    for (uint32_t t0 = 0; t0 < m_tokens; t0 += kMaxGridY) {
+        const uint32_t n = std::min(kMaxGridY, m_tokens - t0);
+        bp::QNormRopeArgs a;
+        a.act = static_cast<uint16_t*>(act);
+        a.w_norms = static_cast<const uint16_t*>(w_norms);
+        a.rope_cs = m->rope_cs;
+        a.q_off = static_cast<uint64_t>(q_off) + static_cast<uint64_t>(t0) * m->q_dim;
+        a.w_off = w_q_norm_off;
+        a.pos_base = pos_base + t0;
+        a.q_dim = m->q_dim;
+        a.eps = m->cfg.rms_eps;
+        if ((st = hip_check(m, bp::launch_q_norm_rope(a, m->cfg.n_head, n, m->stream), "q_norm_rope launch")) != BP_OK)
+            return st;
+    }
+    return BP_OK;
+}
+
+bp_status bp_dispatch_kv_writeback_fused(bp_model* m, const void* act, const void* w_norms,
+                                         uint32_t k_cur_off, uint32_t v_cur_off, uint32_t w_k_norm_off,
+                                         uint32_t layer_il, uint32_t pos_base, uint32_t m_tokens) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act || !w_norms) return fail(BP_ERR_INVALID_ARG, "act/w_norms is NULL");
+    if (layer_il >= m->cfg.n_layer)
+        return fail(BP_ERR_INVALID_ARG, "layer %u >= n_layer %u", layer_il, m->cfg.n_layer);
+    if (m_tokens == 0) return BP_OK;
+    if (static_cast<uint64_t>(pos_base) + m_tokens > m->max_seq)
+        return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens %u > max_seq %u",
+                    pos_base, m_tokens, m->max_seq);
+    const bp::KvView kv = kv_view(m, m->kv_k, layer_il), vv = kv_view(m, m->kv_v, layer_il);
+    for (uint32_t t0 = 0; t0 < m_tokens; t0 += kMaxGridY) {
+        const uint32_t n = std::min(kMaxGridY, m_tokens - t0);
+        bp::KvWritebackArgs a;
+        a.act = static_cast<const uint16_t*>(act);
+        a.w_norms = static_cast<const uint16_t*>(w_norms);
+        a.rope_cs = m->rope_cs;
+        a.k_d = const_cast<float*>(kv.d);
+        a.k_qs = const_cast<int8_t*>(kv.qs);
+        a.v_d = const_cast<float*>(vv.d);
+        a.v_qs = const_cast<int8_t*>(vv.qs);
+        a.k_cur_off = static_cast<uint64_t>(k_cur_off) + static_cast<uint64_t>(t0) * m->kv_dim;
+        a.v_cur_off = static_cast<uint64_t>(v_cur_off) + static_cast<uint64_t>(t0) * m->kv_dim;
+        a.w_off = w_k_norm_off;
+        a.pos_base = pos_base + t0;
+        a.kv_dim = m->kv_dim;
+        a.eps = m->cfg.rms_eps;
+        if ((st = hip_check(m, bp::launch_kv_writeback(a, m->cfg.n_kv_head, n, m->stream),
+                            "kv_writeback launch")) != BP_OK)
+            return st;
+    }
+    return BP_OK;
+}
+
+bp_status bp_dispatch_attention_decode(bp_model* m, void* act, uint32_t q_off, uint32_t out_off,
+                                       uint32_t layer_il, uint32_t pos) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act) return fail(BP_ERR_INVALID_ARG, "act is NULL");
+    if (layer_il >= m->cfg.n_layer)
+        return fail(BP_ERR_INVALID_ARG, "layer %u >= n_layer %u", layer_il, m->cfg.n_layer);
+    if (pos >= m->max_seq)
+        return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens 1 > max_seq %u", pos,
+                    m->max_seq);
+    if ((q_off & 7u) || (out_off & 1u))
+        return fail(BP_ERR_INVALID_ARG, "q_off must be a multiple of 8 and out_off even (aligned f16 rows)");
+    bp::DecodeArgs a;
+    a.q = static_cast<const uint16_t*>(act) + q_off;
+    a.out = static_cast<uint16_t*>(act) + out_off;
+    a.k = kv_view(m, m->kv_k, layer_il);
+    a.v = kv_view(m, m->kv_v, layer_il);
+    a.partials = m->partials;
+    a.tickets = m->tickets;
+    a.kv_dim = m->kv_dim;
+    a.n_keys = pos + 1;   // src/forward.rs:822 (cur_pos = pos + 1)
+    bp::decode_plan(a.n_keys, m->cfg.n_kv_head, m->cu_count, &a.split_len, &a.n_splits);
+    if (static_cast<uint64_t>(a.n_splits) * m->cfg.n_head * (bp::kHeadDim + 2) > m->partials_floats)
+        return fail(BP_ERR_CONFIG, "internal: partials scratch too small for %u splits", a.n_splits);
+    a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:838
+    return hip_check(m, bp::launch_decode(a, m->cfg.n_kv_head, m->stream), "attention_decode launch");
+}
+
+bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t out_off, uint32_t layer_il,
+                                uint32_t pos, uint32_t m_tokens, uint32_t is_prefill) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act) return fail(BP_ERR_INVALID_ARG, "act is NULL");
+    if (layer_il >= m->cfg.n_layer)
+        return fail(BP_ERR_INVALID_ARG, "layer %u >= n_layer %u", layer_il, m->cfg.n_layer);
+    if (m_tokens == 0) return BP_OK;
+    if ((q_off | out_off) & 7u)
+        return fail(BP_ERR_INVALID_ARG, "q_off/out_off must be multiples of 8 (16-byte aligned f16 rows)");
+    const uint64_t rows = is_prefill ? static_cast<uint64_t>(pos) + m_tokens : pos;
+    if (rows > m->max_seq)
+        return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens %u > max_seq %u", pos,
+                    m_tokens, m->max_seq);
+    if (rows == 0) return fail(BP_ERR_INVALID_ARG, "attention over zero cache rows (pos 0, is_prefill 0)");
+    bp::PrefillArgs a;
+    a.q = static_cast<const uint16_t*>(act) + q_off;
+    a.out = static_cast<uint16_t*>(act) + out_off;
+    a.k = kv_view(m, m->kv_k, layer_il);
+    a.v = kv_view(m, m->kv_v, layer_il);
+    a.kv_dim = m->kv_dim;
+    a.q_stride = m->q_dim;
+    a.m_tokens = m_tokens;
+    a.pos = pos;
+    a.causal = is_prefill ? 1u : 0u;
+    a.n_tiles = (m_tokens + 63) / 64;
+    a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:524
+    return hip_check(m, bp::launch_prefill(a, m->cfg.n_kv_head, m->stream), "attention launch");
+}
+
+static bp_status snapshot_copy(bp_model* m, uint32_t pos, uint8_t* payload, uint64_t payload_bytes,
+                               bool to_host) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (pos > m->max_seq)
+        return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos 0 + tokens %u > max_seq %u", pos,
+                    m->max_seq);
+    const uint64_t need = bp_kv_snapshot_payload_bytes(m->cfg.n_layer, m->kv_dim, pos);
+    if (payload_bytes != need)
+        return fail(BP_ERR_CONFIG, "KvSnapshot payload length %llu does not match %llu",
+                    static_cast<unsigned long long>(payload_bytes), static_cast<unsigned long long>(need));
+    if (pos == 0) return BP_OK;   // src/kv_snapshot.rs:212-221, :310-312
+    if (!payload) return fail(BP_ERR_INVALID_ARG, "payload is NULL");
+    const uint64_t d_size = static_cast<uint64_t>(pos) * m->nb_per_row * 4;
+    const uint64_t qs_size = static_cast<uint64_t>(pos) * m->kv_dim;
+    const uint64_t layer_bytes = d_size + qs_size;
+    const uint32_t nl = m->cfg.n_layer;
+    for (uint32_t kind = 0; kind < 2; kind++) {
+        uint8_t* buf = kind == 0 ? m->kv_k : m->kv_v;
+        for (uint32_t il = 0; il < nl; il++) {
+            // payload_offset, src/kv_snapshot.rs:158-169
+            uint8_t* pd = payload + static_cast<uint64_t>(kind) * nl * layer_bytes + il * layer_bytes;
+            uint8_t* pq = pd + d_size;
+            uint8_t* bd = buf + kv_d_word(m, il) * 4;
+            uint8_t* bq = buf + kv_qs_byte(m, il);
+            hipError_t e1 = to_host ? hipMemcpyAsync(pd, bd, d_size, hipMemcpyDeviceToHost, m->stream)
+                                    : hipMemcpyAsync(bd, pd, d_size, hipMemcpyHostToDevice, m->stream);
+            if ((st = hip_check(m, e1, "snapshot copy (d)")) != BP_OK) return st;
+            hipError_t e2 = to_host ? hipMemcpyAsync(pq, bq, qs_size, hipMemcpyDeviceToHost, m->stream)
+                                    : hipMemcpyAsync(bq, pq, qs_size, hipMemcpyHostToDevice, m->stream);
+            if ((st = hip_check(m, e2, "snapshot copy (qs)")) != BP_OK) return st;
+        }
+    }
+    return hip_check(m, hipStreamSynchronize(m->stream), "snapshot sync");
+}
+
+bp_status bp_kv_snapshot_capture(bp_model* m, uint32_t pos, void* payload, uint64_t payload_bytes) {
+    return snapshot_copy(m, pos, static_cast<uint8_t*>(payload), payload_bytes, true);
+}
+
+bp_status bp_kv_snapshot_apply(bp_model* m, uint32_t pos, const void* payload, uint64_t payload_bytes) {
+    return snapshot_copy(m, pos, static_cast<uint8_t*>(const_cast<void*>(payload)), payload_bytes, false);
+}
+
+}  // extern "C"

@@ -1,0 +1,84 @@
+// Internal interface between the host layer (bp_api.cpp) and the gfx950
+// kernels. Every launcher checks nothing: argument validation is the host
+// layer's job, and it has been done by the time a launcher runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace bp {
+
+constexpr uint32_t kHeadDim = 128;   // Bonsai head_dim (src/model.rs:1179-1183)
+constexpr uint32_t kGroup = 4;       // Q heads per KV head (attention_split.wgsl:150)
+constexpr uint32_t kBlock = 32;      // Q8_0 block (src/forward.rs:40-47)
+
+// One (layer, kind) view of a Q8_0 KV buffer: FP32 scales at d (index
+// (row*kv_dim + e)/32), int8 quants at qs (index row*kv_dim + e).
+struct KvView {
+    const float* d;
+    const int8_t* qs;
+};
+
+// q_norm_rope_fused / kv_writeback_fused share the per-head norm+rope stage.
+struct QNormRopeArgs {
+    uint16_t* act;            // f16 bits
+    const uint16_t* w_norms;  // f16 bits
+    const uint16_t* rope_cs;  // f16 bits, [max_seq][64][(cos, sin)]
+    uint64_t q_off;           // element offset of Q (token 0, head 0)
+    uint64_t w_off;           // element offset of w_q_norm
+    uint32_t pos_base;
+    uint32_t q_dim;           // n_head * 128
+    float eps;
+};
+
+struct KvWritebackArgs {
+    const uint16_t* act;
+    const uint16_t* w_norms;
+    const uint16_t* rope_cs;
+    float* k_d;               // layer base of kv_k's d-section
+    int8_t* k_qs;             // layer base of kv_k's qs-section
+    float* v_d;
+    int8_t* v_qs;
+    uint64_t k_cur_off, v_cur_off, w_off;
+    uint32_t pos_base;
+    uint32_t kv_dim;          // n_kv_head * 128
+    float eps;
+};
+
+struct DecodeArgs {
+    const uint16_t* q;        // act + q_off: [n_head][128]
+    uint16_t* out;            // act + out_off: [n_head][128]
+    KvView k, v;              // layer bases
+    float* partials;          // [n_head][n_splits][130]
+    uint32_t* tickets;        // [n_kv_head], zero between launches
+    uint32_t kv_dim;
+    uint32_t n_keys;          // rows attended: pos + 1
+    uint32_t split_len;       // rows per workgroup, multiple of 32
+    uint32_t n_splits;
+    float scale;
+};
+
+struct PrefillArgs {
+    const uint16_t* q;        // act + q_off: [m][n_head][128]
+    uint16_t* out;            // act + out_off
+    KvView k, v;
+    uint32_t kv_dim;
+    uint32_t q_stride;        // n_head * 128
+    uint32_t m_tokens;
+    uint32_t pos;             // first query's RoPE/cache position when causal
+    uint32_t causal;          // 1: token m sees rows [0, pos+m]; 0: rows [0, pos)
+    uint32_t n_tiles;         // ceil(m_tokens / 64)
+    float scale;
+};
+
+hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t m_tokens,
+                              hipStream_t s);
+hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uint32_t m_tokens,
+                               hipStream_t s);
+// Partial buffer floats needed by a decode over n_keys rows.
+void decode_plan(uint32_t n_keys, uint32_t n_kv_head, int cu_count, uint32_t* split_len,
+                 uint32_t* n_splits);
+hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s);
+
+}  // namespace bp

@@ -1,0 +1,113 @@
+// Q-side norm+RoPE and K/V writeback into the Q8_0 cache, for gfx950.
+//
+// Restates src/shaders/q_norm_rope_fused.wgsl and
+// src/shaders/kv_writeback_fused.wgsl (reference repository) with a
+// wave64-native layout: ONE wavefront per (head, token), lane j holding the
+// RoPE pair (x[j], x[j+64]). The pair partner therefore lives in the same
+// lane (no LDS round trip), the 128-element sum of squares is a 6-step xor
+// butterfly, and each 32-element Q8_0 block is one 32-lane half of the wave
+// (blocks 0/2 in lanes 0-31, blocks 1/3 in lanes 32-63).
+//
+// Bit-exactness. Every f32 operation is one IEEE-rounded op in the order of
+// the reference shader (no contraction, correctly rounded sqrt and divide),
+// and the RMSNorm reduction uses the fixed butterfly order
+//   s_j = x_j*x_j + x_{j+64}*x_{j+64};  s += shfl_xor(s, 32, 16, 8, 4, 2, 1)
+// so cache bytes and f16 outputs match the CPU oracle bit for bit.
+#include "bp_device.hpp"
+#include "bp_kernels.hpp"
+
+namespace bp {
+namespace {
+
+// RMSNorm(x) * w followed by NEOX RoPE, for the pair (x0 = x[j], x1 = x[j+64]).
+// q_norm_rope_fused.wgsl:53-93 / kv_writeback_fused.wgsl:69-108.
+__device__ __forceinline__ void norm_rope_pair(float x0, float x1, float w0, float w1, float c,
+                                               float s, float eps, float& o0, float& o1) {
+    float sq = x0 * x0 + x1 * x1;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sq = sq + __shfl_xor(sq, off);
+    float inv_h = 1.0f / sqrtf(sq / 128.0f + eps);
+    float n0 = x0 * inv_h * w0;
+    float n1 = x1 * inv_h * w1;
+    o0 = n0 * c - n1 * s;   // kv_writeback_fused.wgsl:102
+    o1 = n0 * s + n1 * c;   // kv_writeback_fused.wgsl:107
+}
+
+// Q8_0-quantize the pair and store it; lanes 0-31 own blocks 0 and 2, lanes
+// 32-63 blocks 1 and 3 (kv_writeback_fused.wgsl:118-200).
+__device__ __forceinline__ void quantize_store_pair(float x0, float x1, int lane, float* d_row,
+                                                    int8_t* qs_row) {
+    float a0 = fabsf(x0), a1 = fabsf(x1);
+#pragma unroll
+    for (int off = 1; off <= 16; off <<= 1) {
+        a0 = fmaxf(a0, __shfl_xor(a0, off));
+        a1 = fmaxf(a1, __shfl_xor(a1, off));
+    }
+    float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
+    float i0 = d0 > 0.0f ? 1.0f / d0 : 0.0f;
+    float i1 = d1 > 0.0f ? 1.0f / d1 : 0.0f;
+    int q0 = static_cast<int>(fminf(fmaxf(rintf(x0 * i0), -127.0f), 127.0f));
+    int q1 = static_cast<int>(fminf(fmaxf(rintf(x1 * i1), -127.0f), 127.0f));
+    // Gather 4 consecutive lanes' bytes into one little-endian word.
+    uint32_t p = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8);
+    int b = lane & ~3;
+    uint32_t p0 = __shfl(p, b), p1 = __shfl(p, b + 1), p2 = __shfl(p, b + 2), p3 = __shfl(p, b + 3);
+    if ((lane & 3) == 0) {
+        uint32_t lo = (p0 & 0xffu) | ((p1 & 0xffu) << 8) | ((p2 & 0xffu) << 16) | ((p3 & 0xffu) << 24);
+        uint32_t hi = (p0 >> 8) | ((p1 >> 8) << 8) | ((p2 >> 8) << 16) | ((p3 >> 8) << 24);
+        *reinterpret_cast<uint32_t*>(qs_row + lane) = lo;
+        *reinterpret_cast<uint32_t*>(qs_row + 64 + lane) = hi;
+    }
+    if ((lane & 31) == 0) {
+        int blk = lane >> 5;          // 0 or 1
+        d_row[blk] = d0;              // elements [32*blk, 32*blk+32)
+        d_row[blk + 2] = d1;          // elements [64+32*blk, ...)
+    }
+}
+
+__global__ __launch_bounds__(64) void q_norm_rope_kernel(QNormRopeArgs a) {
+    const int j = threadIdx.x;
+    const uint32_t head = blockIdx.x, tok = blockIdx.y;
+    uint16_t* q = a.act + a.q_off + static_cast<uint64_t>(tok) * a.q_dim + head * kHeadDim;
+    const uint16_t* cs =
+        a.rope_cs + static_cast<uint64_t>(a.pos_base + tok) * kHeadDim + 2 * j;
+    float o0, o1;
+    norm_rope_pair(h2f(q[j]), h2f(q[j + 64]), h2f(a.w_norms[a.w_off + j]),
+                   h2f(a.w_norms[a.w_off + j + 64]), h2f(cs[0]), h2f(cs[1]), a.eps, o0, o1);
+    q[j] = f2h(o0);          // q_norm_rope_fused.wgsl:95
+    q[j + 64] = f2h(o1);
+}
+
+__global__ __launch_bounds__(64) void kv_writeback_kernel(KvWritebackArgs a) {
+    const int j = threadIdx.x;
+    const uint32_t head = blockIdx.x, tok = blockIdx.y;
+    const uint64_t tok_off = static_cast<uint64_t>(tok) * a.kv_dim + head * kHeadDim;
+    const uint16_t* k = a.act + a.k_cur_off + tok_off;
+    const uint16_t* v = a.act + a.v_cur_off + tok_off;
+    const uint64_t row = static_cast<uint64_t>(a.pos_base) + tok;
+    const uint16_t* cs = a.rope_cs + row * kHeadDim + 2 * j;
+    float k0, k1;
+    norm_rope_pair(h2f(k[j]), h2f(k[j + 64]), h2f(a.w_norms[a.w_off + j]),
+                   h2f(a.w_norms[a.w_off + j + 64]), h2f(cs[0]), h2f(cs[1]), a.eps, k0, k1);
+    const uint64_t nb_row = a.kv_dim / kBlock;
+    const uint64_t d_idx = row * nb_row + head * (kHeadDim / kBlock);
+    const uint64_t qs_idx = row * a.kv_dim + head * kHeadDim;
+    quantize_store_pair(k0, k1, j, a.k_d + d_idx, a.k_qs + qs_idx);
+    quantize_store_pair(h2f(v[j]), h2f(v[j + 64]), j, a.v_d + d_idx, a.v_qs + qs_idx);
+}
+
+}  // namespace
+
+hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t m_tokens,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(q_norm_rope_kernel, dim3(n_head, m_tokens), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uint32_t m_tokens,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(kv_writeback_kernel, dim3(n_kv_head, m_tokens), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace bp

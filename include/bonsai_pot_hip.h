@@ -1,0 +1,146 @@
+/*
+ * bonsai_pot_hip.h — C ABI of the MI355X (gfx950) attention hot path of
+ * bonsai-pot: Q/K RMSNorm + NEOX RoPE, Q8_0 KV-cache writeback, split-K
+ * decode attention and causal (chunked) prefill attention.
+ *
+ * The entry points replace the reference's crate-private dispatch helpers
+ * (paths relative to the reference repository root) one for one:
+ *
+ *   bp_dispatch_q_norm_rope_fused    <- dispatch_q_norm_rope_fused   src/forward.rs:392-413
+ *   bp_dispatch_kv_writeback_fused   <- dispatch_kv_writeback_fused  src/forward.rs:359-388
+ *   bp_dispatch_attention_decode     <- split+merge block in layer_post_kv_in_pass
+ *                                       src/forward.rs:820-857
+ *   bp_dispatch_attention            <- dispatch_attention           src/forward.rs:501-532
+ *   bp_model_create / _destroy       <- KV / RoPE / partials part of Model::load_with_options
+ *                                       src/model.rs:1148-1248
+ *   bp_kv_snapshot_capture / _apply  <- kv_snapshot::capture / apply src/kv_snapshot.rs:203-372
+ *   bp_check_device                  <- Model::check_device          src/model.rs:1733-1741
+ *   bp_debug_lose_device             <- Model::__destroy_device_for_test src/model.rs:1746-1751
+ *
+ * Conventions (the same as the reference's Params structs):
+ *   - `act` is one f16 buffer; *_off arguments are f16-ELEMENT offsets into it.
+ *   - `w_norms` is the f16 norm-weight buffer; w_*_norm_off are element offsets.
+ *   - kv_k / kv_v are owned by the model and keep the reference byte layout
+ *     (src/forward.rs:40-58, src/model.rs:1167-1215):
+ *       [d-section: n_layer*max_seq*(kv_dim/32) f32][qs-section: n_layer*max_seq*kv_dim i8]
+ *   - All calls are asynchronous on the model's stream, stream-ordered, and
+ *     never allocate device memory. One model is driven by one host thread at
+ *     a time (src/session.rs:67-88).
+ *   - Every call returns a bp_status; nothing unwinds across the ABI. After a
+ *     device fault the model latches "lost" and every later call returns
+ *     BP_ERR_DEVICE_LOST (src/model.rs:1087-1098, :1733-1741).
+ */
+#ifndef BONSAI_POT_HIP_H
+#define BONSAI_POT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t bp_status;
+/* Status codes; each maps onto a PotError variant (src/error.rs:8-38). */
+#define BP_OK                    0
+#define BP_ERR_CONFIG           -1  /* PotError::Config */
+#define BP_ERR_CONTEXT_OVERFLOW -2  /* PotError::ContextOverflow */
+#define BP_ERR_INVALID_ARG      -3  /* PotError::Config (bad pointer / offset) */
+#define BP_ERR_HIP              -4  /* runtime error other than device loss */
+#define BP_ERR_DEVICE_LOST      -5  /* PotError::DeviceLost */
+#define BP_ERR_OUT_OF_MEMORY    -6  /* allocation at model creation failed */
+#define BP_ERR_NO_DEVICE        -7  /* PotError::NoAdapter */
+
+/* Attention-side subset of Config (src/model.rs:568-656). */
+typedef struct bp_config {
+    uint32_t n_layer;
+    uint32_t n_head;         /* query heads (32 for Bonsai 4B/8B) */
+    uint32_t n_kv_head;      /* KV heads (8); n_head/n_kv_head must be 4 */
+    uint32_t head_dim;       /* must be 128 (src/model.rs:1179-1183) */
+    float rms_eps;           /* 1e-6 for Bonsai */
+    float rope_freq_base;    /* 1e6 for Bonsai */
+} bp_config;
+
+typedef struct bp_model bp_model;
+
+/* Creates the device-side state the attention path owns: kv_k, kv_v (zeroed),
+ * the f16 RoPE table for positions [0, max_seq) and the split-K partials
+ * scratch. `device` is a HIP device ordinal. */
+bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp_model** out);
+void bp_model_destroy(bp_model* model);
+
+/* Stream all later calls are ordered on (a hipStream_t; NULL = the null stream). */
+bp_status bp_model_set_stream(bp_model* model, void* stream);
+/* Blocks until the model's stream is idle; latches device loss on failure. */
+bp_status bp_model_synchronize(bp_model* model);
+
+/* Device pointers and sizes of the model-owned buffers (for snapshotting,
+ * tests and the caller's own bookkeeping). Any out-pointer may be NULL. */
+bp_status bp_model_kv_buffers(const bp_model* model, void** kv_k, void** kv_v, uint64_t* bytes_each);
+bp_status bp_model_rope_table(const bp_model* model, const void** rope_cs_f16);
+uint32_t bp_model_max_seq(const bp_model* model);
+
+/* Layer base offsets inside kv_k / kv_v: (u32-word offset of the d-section,
+ * byte offset of the qs-section) — src/forward.rs:48-58 (u64 here). */
+bp_status bp_kv_layer_offsets(uint32_t n_layer, uint32_t kv_dim, uint32_t max_seq, uint32_t il,
+                              uint64_t* d_word_offset, uint64_t* qs_byte_offset);
+/* Bytes of one KV buffer: n_layer*max_seq*(kv_dim/32)*4 + n_layer*max_seq*kv_dim
+ * (src/model.rs:1184-1187). */
+uint64_t bp_kv_buffer_bytes(uint32_t n_layer, uint32_t kv_dim, uint32_t max_seq);
+
+/* q_norm_rope_fused (src/shaders/q_norm_rope_fused.wgsl): for m_tokens tokens
+ * starting at RoPE position pos_base, RMSNorm each 128-wide Q head, multiply by
+ * w_q_norm, apply NEOX RoPE, and write f16 back in place at act[q_off...]. */
+bp_status bp_dispatch_q_norm_rope_fused(bp_model* model, void* act, const void* w_norms,
+                                        uint32_t q_off, uint32_t w_q_norm_off,
+                                        uint32_t pos_base, uint32_t m_tokens);
+
+/* kv_writeback_fused (src/shaders/kv_writeback_fused.wgsl): for m_tokens
+ * tokens written at cache rows [pos_base, pos_base+m_tokens) of layer
+ * layer_il: K = RoPE(RMSNorm(k)*w_k_norm), V = v; both Q8_0-quantized
+ * (d = amax/127 FP32, q = clamp(rne(x*(1/d)), +-127)) into kv_k / kv_v. */
+bp_status bp_dispatch_kv_writeback_fused(bp_model* model, const void* act, const void* w_norms,
+                                         uint32_t k_cur_off, uint32_t v_cur_off,
+                                         uint32_t w_k_norm_off, uint32_t layer_il,
+                                         uint32_t pos_base, uint32_t m_tokens);
+
+/* Single-token decode attention at step position `pos`: the query at
+ * act[q_off] ([n_head][128] f16) attends cache rows [0, pos] of layer
+ * layer_il (pos+1 rows, src/forward.rs:822), split-K over the sequence with a
+ * log-sum-exp merge; writes f16 [n_head][128] at act[out_off]. */
+bp_status bp_dispatch_attention_decode(bp_model* model, void* act, uint32_t q_off,
+                                       uint32_t out_off, uint32_t layer_il, uint32_t pos);
+
+/* Batched attention (src/shaders/attention.wgsl, src/forward.rs:501-532) over
+ * m_tokens query tokens at act[q_off] ([m][n_head][128] f16), writing
+ * act[out_off] ([m][n_head][128] f16). Token m attends cache rows
+ * [0, cur) with cur = is_prefill ? pos + m + 1 : pos. With pos == 0 and
+ * is_prefill != 0 this is the reference's causal prefill from an empty cache;
+ * pos > 0 is causal chunked prefill over an existing cache (the reference
+ * reaches that result only one token at a time, src/forward.rs:914-967). */
+bp_status bp_dispatch_attention(bp_model* model, void* act, uint32_t q_off, uint32_t out_off,
+                                uint32_t layer_il, uint32_t pos, uint32_t m_tokens,
+                                uint32_t is_prefill);
+
+/* BONSAIKV v1 payload (src/kv_snapshot.rs:8-20): for kind in {K, V}, for each
+ * layer: pos*(kv_dim/32)*4 bytes of d, then pos*kv_dim bytes of qs.
+ * `payload` is host memory of exactly bp_kv_snapshot_payload_bytes(). Both
+ * calls synchronize the model's stream. */
+uint64_t bp_kv_snapshot_payload_bytes(uint32_t n_layer, uint32_t kv_dim, uint32_t pos);
+bp_status bp_kv_snapshot_capture(bp_model* model, uint32_t pos, void* payload, uint64_t payload_bytes);
+bp_status bp_kv_snapshot_apply(bp_model* model, uint32_t pos, const void* payload, uint64_t payload_bytes);
+
+/* Device-loss latch (src/model.rs:1733-1741) and its test hook
+ * (src/model.rs:1746-1751; host-side only: marks the model lost without
+ * touching the GPU). */
+bp_status bp_check_device(const bp_model* model);
+bp_status bp_debug_lose_device(bp_model* model);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* bp_last_error(void);
+const char* bp_status_name(bp_status status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BONSAI_POT_HIP_H */

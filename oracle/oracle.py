@@ -1,0 +1,206 @@
+"""numpy-facing ctypes wrapper of the CPU oracle (oracle/bp_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker — never by the product path.
+
+Arrays: f16 data is passed as numpy uint16 bit patterns (or float16 arrays,
+viewed as uint16); KV buffers are uint8 arrays of the reference byte layout.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbp_oracle.so")
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+if not os.path.exists(LIB_PATH):
+    build()
+_lib = ctypes.CDLL(LIB_PATH)
+
+_u32, _u64, _f32, _vp = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p
+
+
+class KvWritebackParams(ctypes.Structure):
+    """KvWritebackFusedParams, src/model.rs:265-276."""
+    _fields_ = [(n, _u32) for n in ("k_cur_off", "v_cur_off", "w_k_norm_off", "rope_offset",
+                                     "dst_d_word_offset", "dst_qs_byte_offset", "pos_base",
+                                     "kv_dim", "nb_per_row")] + [("eps", _f32)]
+
+
+class QNormRopeParams(ctypes.Structure):
+    """QNormRopeFusedParams, src/model.rs:255-262."""
+    _fields_ = [(n, _u32) for n in ("q_off", "w_q_norm_off", "rope_offset", "pos_base",
+                                     "q_dim")] + [("eps", _f32)]
+
+
+class AttnSplitParams(ctypes.Structure):
+    """AttnSplitParams (src/model.rs:213-226) + AttnMergeParams.out_offset."""
+    _fields_ = [(n, _u32) for n in ("head_dim", "n_head", "n_kv_head", "pos", "kv_stride",
+                                     "q_offset", "k_d_word_offset", "k_qs_byte_offset",
+                                     "v_d_word_offset", "v_qs_byte_offset", "n_chunks_active")] + \
+               [("scale", _f32), ("out_offset", _u32)]
+
+
+class AttnParams(ctypes.Structure):
+    """AttnParams, src/model.rs:195-210."""
+    _fields_ = [(n, _u32) for n in ("head_dim", "n_head", "n_kv_head", "pos", "kv_stride",
+                                     "q_offset", "k_d_word_offset", "k_qs_byte_offset",
+                                     "v_d_word_offset", "v_qs_byte_offset", "out_offset")] + \
+               [("scale", _f32), ("m_tokens", _u32), ("is_prefill", _u32)]
+
+
+def _sig(name, res, args):
+    f = getattr(_lib, name)
+    f.restype, f.argtypes = res, args
+    return f
+
+
+_f32_to_f16 = _sig("bpo_f32_to_f16", ctypes.c_uint16, [_f32])
+_f16_to_f32 = _sig("bpo_f16_to_f32", _f32, [ctypes.c_uint16])
+_f32_to_f16_arr = _sig("bpo_f32_to_f16_array", None, [_vp, _vp, ctypes.c_size_t])
+_f16_to_f32_arr = _sig("bpo_f16_to_f32_array", None, [_vp, _vp, ctypes.c_size_t])
+_rope = _sig("bpo_build_rope_table", None, [_u32, _f32, _u32, _vp, _vp])
+_layer_off = _sig("bpo_kv_layer_offsets", None, [_u32, _u32, _u32, _u32, ctypes.POINTER(_u64),
+                                                 ctypes.POINTER(_u64)])
+_buf_bytes = _sig("bpo_kv_buffer_bytes", _u64, [_u32, _u32, _u32])
+_snap_bytes = _sig("bpo_snapshot_payload_bytes", _u64, [_u32, _u32, _u32])
+_snap_off = _sig("bpo_snapshot_payload_offset", _u64, [_u32, _u32, _u32, _u32, _u32, _u32])
+_snap_cap = _sig("bpo_snapshot_capture", None, [_u32, _u32, _u32, _u32, _vp, _vp, _vp])
+_snap_apply = _sig("bpo_snapshot_apply", None, [_u32, _u32, _u32, _u32, _vp, _vp, _vp])
+_quant = _sig("bpo_quantize_q8_0_block", None, [_vp, _vp, _vp])
+_kvwb = _sig("bpo_kv_writeback_fused", None, [ctypes.POINTER(KvWritebackParams), _vp, _vp, _vp,
+                                             _vp, _vp, _u32, _u32])
+_qnr = _sig("bpo_q_norm_rope_fused", None, [ctypes.POINTER(QNormRopeParams), _vp, _vp, _vp, _u32,
+                                           _u32])
+_split = _sig("bpo_attention_split_merge", None, [ctypes.POINTER(AttnSplitParams), _vp, _vp, _vp,
+                                                  _vp, _vp])
+_attn = _sig("bpo_attention", None, [ctypes.POINTER(AttnParams), _vp, _vp, _vp, _vp, _u32, _vp,
+                                    _vp])
+_fill = _sig("bpo_fill_normal_f16", None, [_u64, _f32, _f32, _vp, ctypes.c_size_t])
+
+
+def _ptr(a):
+    return a.ctypes.data_as(_vp) if a is not None else None
+
+
+def _u16(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint16) if a.dtype == np.float16 else a
+
+
+# ---- conversions -------------------------------------------------------------
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    _f32_to_f16_arr(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = _u16(h)
+    out = np.empty(h.shape, np.float32)
+    _f16_to_f32_arr(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+# ---- tables / layout -----------------------------------------------------------
+def rope_table(head_dim: int, base: float, max_seq: int):
+    """(f32 table, f16-bit table), each [max_seq * head_dim]."""
+    f = np.empty(max_seq * head_dim, np.float32)
+    h = np.empty(max_seq * head_dim, np.uint16)
+    _rope(head_dim, base, max_seq, _ptr(f), _ptr(h))
+    return f, h
+
+
+def kv_layer_offsets(n_layer, kv_dim, max_seq, il):
+    d, q = _u64(), _u64()
+    _layer_off(n_layer, kv_dim, max_seq, il, ctypes.byref(d), ctypes.byref(q))
+    return d.value, q.value
+
+
+def kv_buffer_bytes(n_layer, kv_dim, max_seq):
+    return _buf_bytes(n_layer, kv_dim, max_seq)
+
+
+def snapshot_payload_bytes(n_layer, kv_dim, pos):
+    return _snap_bytes(n_layer, kv_dim, pos)
+
+
+def snapshot_payload_offset(n_layer, kv_dim, pos, kind, il, sect):
+    return _snap_off(n_layer, kv_dim, pos, kind, il, sect)
+
+
+def snapshot_capture(n_layer, kv_dim, max_seq, pos, kv_k, kv_v) -> np.ndarray:
+    out = np.empty(snapshot_payload_bytes(n_layer, kv_dim, pos), np.uint8)
+    _snap_cap(n_layer, kv_dim, max_seq, pos, _ptr(kv_k), _ptr(kv_v), _ptr(out))
+    return out
+
+
+def snapshot_apply(n_layer, kv_dim, max_seq, pos, payload, kv_k, kv_v) -> None:
+    payload = np.ascontiguousarray(payload, dtype=np.uint8)
+    _snap_apply(n_layer, kv_dim, max_seq, pos, _ptr(payload), _ptr(kv_k), _ptr(kv_v))
+
+
+def quantize_block(x):
+    """Q8_0 one block of 32 f32 values -> (d, int8[32])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.shape == (32,)
+    d = np.zeros(1, np.float32)
+    q = np.zeros(32, np.int8)
+    _quant(_ptr(x), _ptr(d), _ptr(q))
+    return float(d[0]), q
+
+
+# ---- kernels ---------------------------------------------------------------------
+def kv_writeback_fused(p: KvWritebackParams, act, w_norms, rope_cs, kv_k, kv_v, n_kv_head,
+                       m_tokens) -> None:
+    """In place on kv_k / kv_v (uint8 arrays)."""
+    act, w_norms, rope_cs = _u16(act), _u16(w_norms), _u16(rope_cs)
+    assert kv_k.dtype == np.uint8 and kv_v.dtype == np.uint8
+    _kvwb(ctypes.byref(p), _ptr(act), _ptr(w_norms), _ptr(rope_cs), _ptr(kv_k), _ptr(kv_v),
+          n_kv_head, m_tokens)
+
+
+def q_norm_rope_fused(p: QNormRopeParams, act, w_norms, rope_cs, n_head, m_tokens) -> None:
+    """In place on act (uint16 array)."""
+    assert act.dtype == np.uint16 and act.flags.c_contiguous
+    w_norms, rope_cs = _u16(w_norms), _u16(rope_cs)
+    _qnr(ctypes.byref(p), _ptr(act), _ptr(w_norms), _ptr(rope_cs), n_head, m_tokens)
+
+
+def attention_split_merge(p: AttnSplitParams, act, kv_k, kv_v):
+    """Returns (f16-bit output [n_head*head_dim], f32 output)."""
+    act = _u16(act)
+    out16 = act.copy()
+    out32 = np.empty(p.n_head * p.head_dim, np.float32)
+    _split(ctypes.byref(p), _ptr(act), _ptr(kv_k), _ptr(kv_v), _ptr(out16), _ptr(out32))
+    o = p.out_offset
+    return out16[o:o + p.n_head * p.head_dim].copy(), out32
+
+
+def attention(p: AttnParams, act, kv_k, kv_v, tokens=None):
+    """f32 outputs [n_tokens, n_head*head_dim] for the selected tokens (all if None)."""
+    act = _u16(act)
+    if tokens is None:
+        n = p.m_tokens
+        tok = None
+    else:
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32)
+        n = tok.size
+    out32 = np.empty((n, p.n_head * p.head_dim), np.float32)
+    _attn(ctypes.byref(p), _ptr(act), _ptr(kv_k), _ptr(kv_v), _ptr(tok), n, None, _ptr(out32))
+    return out32
+
+
+def fill_normal_f16(seed: int, n: int, mean=0.0, std=1.0) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    _fill(seed, mean, std, _ptr(out), n)
+    return out

@@ -99,21 +99,34 @@ def time_region(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
-def per_launch_us(torch, launch, n_launch):
-    """Average device duration of single launches, each bracketed by HIP events
-    on the stream the kernel runs on."""
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_launch)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_launch)]
-    for i in range(n_launch):
-        starts[i].record()
-        launch(i)
-        ends[i].record()
+def per_launch_us(torch, b, launch, n_launch, replays=5):
+    """Average device time of one launch: n_launch launches (rotating layers) are
+    captured in a HIP graph and replayed between two HIP events recorded on the
+    stream the kernels run on, so host launch latency is excluded (inter-kernel
+    gaps of graph dispatch are included)."""
+    g = make_graph(torch, b, lambda: [launch(i) for i in range(n_launch)])
+    g.replay()
     torch.cuda.synchronize()
-    ts = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))
-    return sum(ts) / len(ts), ts[len(ts) // 2]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (replays * n_launch)
 
 
 def run_decode_step(b: "Bench", pos: int, layers):
+    """One decode step over `layers`: per layer q_norm_rope + kv_writeback of row
+    `pos` + attention over rows [0, pos], as the fused two-launch entry point."""
+    m = b.model
+    for il in layers:
+        m.dispatch_attention_decode_step(b.a, b.wp, b.q_off, b.k_off, b.v_off, b.out_off, 0, 128, il, pos)
+
+
+def run_decode_step_unfused(b: "Bench", pos: int, layers):
+    """The same step as the reference's dispatch sequence (three entry points)."""
     m = b.model
     for il in layers:
         m.dispatch_q_norm_rope_fused(b.a, b.wp, b.q_off, 0, pos, 1)
@@ -147,21 +160,25 @@ def bench_decode(torch, args, ctx, n_layer, graph_ok=True):
     body = lambda: run_decode_step(b, pos, layers)
     eager_s = time_region(torch, body, max(3, args.steps // 5), 2)
     graph_s = None
+    unfused_s = None
     if graph_ok and not args.no_graph:
         g = make_graph(torch, b, body)
         graph_s = time_region(torch, g.replay, args.steps, args.warmup)
+        gu = make_graph(torch, b, lambda: run_decode_step_unfused(b, pos, layers))
+        unfused_s = time_region(torch, gu.replay, args.steps, args.warmup)
     step_s = graph_s if graph_s is not None else eager_s
     # dominant kernel: decode attention alone, per launch, rotating layers
     n_l = 4 * n_layer
-    avg_us, med_us = per_launch_us(
-        torch, lambda i: b.model.dispatch_attention_decode(b.a, b.q_off, b.out_off, i % n_layer, pos), n_l)
+    avg_us = per_launch_us(
+        torch, b, lambda i: b.model.dispatch_attention_decode(b.a, b.q_off, b.out_off, i % n_layer, pos), n_l)
     kbytes = decode_bytes(pos + 1)
     res = {
         "ctx": ctx, "n_keys": pos + 1, "layers": n_layer,
         "ms_per_step": step_s * 1e3, "ms_per_step_eager": eager_s * 1e3,
         "ms_per_step_graph": None if graph_s is None else graph_s * 1e3,
+        "ms_per_step_graph_unfused": None if unfused_s is None else unfused_s * 1e3,
         "step_GBps": step_bytes / step_s / 1e9,
-        "kernel_us_avg": avg_us, "kernel_us_median": med_us,
+        "kernel_us_avg": avg_us,
         "kernel_bytes": kbytes, "kernel_GBps": kbytes / (avg_us * 1e-6) / 1e9,
     }
     res["kernel_frac_hbm"] = res["kernel_GBps"] / HBM_PEAK_GBS
@@ -178,12 +195,12 @@ def bench_prefill(torch, args, m, pos):
     for i in range(3):
         b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True)
     torch.cuda.synchronize()
-    avg_us, med_us = per_launch_us(
-        torch, lambda i: b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True), n)
+    avg_us = per_launch_us(
+        torch, b, lambda i: b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True), n)
     tflops = flops / (avg_us * 1e-6) / 1e12
     b.model.close()
     return {"m_tokens": m, "pos_base": pos, "flops": flops, "kernel_us_avg": avg_us,
-            "kernel_us_median": med_us, "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS}
+            "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS}
 
 
 def cpu_baseline(seconds=10.0):
@@ -261,7 +278,7 @@ def main():
         "dtype": "f32 (i8 Q8_0 cache, f16 q/out)",
         "data": "synthetic (seeded N(0,1) q/k/v through kv_writeback; no model weights)",
         "config": {"workload": "configs[1]: Bonsai-4B decode attention, 36 layers, ctx 4096, batch 1 "
-                               "(q_norm_rope + kv_writeback + split-K decode per layer, HIP graph)",
+                               "(fused q_norm_rope + kv_writeback + split-K decode per layer, HIP graph)",
                    "n_head": 32, "n_kv_head": 8, "head_dim": 128, "ctx": 4096, "layers": 36,
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": d4["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -62,6 +62,8 @@ _SIGS = {
     "bp_dispatch_q_norm_rope_fused": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
     "bp_dispatch_kv_writeback_fused": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_attention_decode": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_attention_decode_step": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                                  _u32]),
     "bp_dispatch_attention": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_kv_snapshot_payload_bytes": (_u64, [_u32, _u32, _u32]),
     "bp_kv_snapshot_capture": (_i32, [_vp, _u32, _vp, _u64]),
@@ -155,6 +157,14 @@ class Model:
     def dispatch_attention_decode(self, act: int, q_off: int, out_off: int, layer_il: int,
                                   pos: int) -> None:
         _check(lib.bp_dispatch_attention_decode(self._h, act, q_off, out_off, layer_il, pos))
+
+    def dispatch_attention_decode_step(self, act: int, w_norms: int, q_off: int, k_cur_off: int,
+                                       v_cur_off: int, out_off: int, w_q_norm_off: int,
+                                       w_k_norm_off: int, layer_il: int, pos: int) -> None:
+        """q_norm_rope + kv_writeback + decode attention for one token, fused."""
+        _check(lib.bp_dispatch_attention_decode_step(self._h, act, w_norms, q_off, k_cur_off,
+                                                     v_cur_off, out_off, w_q_norm_off,
+                                                     w_k_norm_off, layer_il, pos))
 
     def dispatch_attention(self, act: int, q_off: int, out_off: int, layer_il: int, pos: int,
                            m_tokens: int, is_prefill: bool) -> None:

@@ -1,41 +1,57 @@
 // Single-token decode attention over the Q8_0 KV cache (gfx950).
 //
 // Same result as src/shaders/attention_split.wgsl + attention_merge.wgsl
-// (reference repository): scores s_t = (q . k_t) / sqrt(128) over rows
-// t in [0, n_keys), softmax in f32, o = sum p_t v_t, f16 output. The work
-// decomposition is MI355X-first instead of the reference's 16-row chunks:
+// (reference repository): scores s_t = (q . k_t) / sqrt(128) over the cache
+// rows, softmax in f32, o = sum p_t v_t, f16 output. Two passes:
 //
-//  * grid = (n_splits, n_kv_head); one 256-thread workgroup owns one KV head
-//    (its 4 GQA query heads) and `split_len` consecutive rows; n_splits is
-//    chosen so the launch covers the 256 CUs about twice.
+// Split pass (decode_split_kernel) — one 256-thread workgroup per (KV head,
+// range of `split_len` rows), the 1-D grid ordered XCD-aware:
 //  * Each wave streams its own rows with no workgroup barrier in the main
 //    loop: a wave "round" is 8 rows, lane (slot = lane>>3, seg = lane&7)
 //    reading the 16 contiguous qs bytes of dims [16 seg, 16 seg + 16) of its
 //    row plus that block's FP32 scale — eight full 128-byte row segments per
 //    load instruction. Waves interleave rounds (wave w takes rounds w, w+4,..)
-//    and the loads of the next batch of 2 rounds are issued before the current
-//    batch is consumed (register double buffering).
-//  * int8 -> f32 uses the unsigned-byte converts on bytes xor 0x80
-//    (u = q + 128); the +128 bias is removed algebraically:
-//      q.k = sum q_i u_i - 128 sum q_i,   sum_t p_t v_t = sum_t p_t u_t - 128 sum_t p_t.
-//  * Online softmax in the exp2 domain; the row max is shared by the whole
-//    wave (3 xor shuffles), so the per-lane running sums need no reduction
-//    until the end, and O is rescaled only when some max moved.
-//  * End of split: shuffles reduce O over the 8 row slots, LDS merges the 4
-//    waves (log-sum-exp), and with more than one split the last workgroup of a
-//    KV head to finish (atomic ticket) merges all splits in parallel and resets
-//    the ticket (attention_merge.wgsl:85-129), so one launch does the decode.
-#include "bp_device.hpp"
+//    and the next batch of kRounds rounds is loaded before the current one is
+//    consumed (register double buffering). Loads are never predicated: rows
+//    past the range are clamped onto its last row and masked by their score.
+//  * q.k runs on v_dot2_f32_f16: q is f16 already, and each K byte pair
+//    becomes an exact f16 pair with one v_perm_b32 — byte (k xor 0x80) under
+//    exponent byte 0x64 is the f16 value 1152 + k — so
+//      q.k = dot2(q, 1152 + k) - 1152 * sum(q).
+//    p.v stays in f32 FMAs (unsigned-byte converts, the same +128 bias
+//    removed algebraically) so the softmax weights are never rounded to f16.
+//  * Online softmax in the exp2 domain; the batch max is shared by the whole
+//    wave, so running sums need no cross-lane reduction until the end and O
+//    is rescaled only when some max moved. Lane reductions use DPP / swizzle.
+//  * The 4 waves merge in LDS (log-sum-exp) into one partial (o[128], m, l)
+//    per query head, written with plain stores; with a single split the
+//    output is written directly and the merge pass is skipped.
+//
+// Merge pass (decode_merge_kernel) — one 64-lane workgroup per (query head,
+// 32-dim chunk): log-sum-exp over the splits (attention_merge.wgsl:85-129),
+// every partial load issued up front.
+//
+// Fused step (launch_decode_step): the split pass also runs q_norm_rope on
+// the 4 query heads of its KV head (same code as the standalone kernel, so the
+// same bits) and, in the last split's workgroup, the kv_writeback of the new
+// row `pos`; it streams rows [0, pos). The merge pass then adds row `pos`
+// (whose bytes are in the cache by then) and writes the normalized q into
+// act. One decode step is two launches instead of four.
 #include "bp_kernels.hpp"
+#include "bp_norm_rope.hpp"
 
 namespace bp {
 namespace {
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kRounds = 2;                 // rounds (8 rows each) per wave batch
-constexpr int kPartStride = kHeadDim + 2;  // o[128], m, l
-constexpr int kMaxMergeSplits = 256;
+constexpr int kRounds = 4;                 // rounds (8 rows each) per wave batch
+constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, pad (16-byte aligned rows)
+constexpr int kMaxSplits = 64;
+constexpr uint32_t kExp64 = 0x64646464u;
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct alignas(16) Q16 { uint32_t w[4]; };
 
@@ -47,42 +63,134 @@ struct Batch {
 __device__ __forceinline__ float ub(uint32_t w, int i) {   // v_cvt_f32_ubyte{i}
     return static_cast<float>((w >> (8 * i)) & 0xffu);
 }
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+// Sum over the 8 lanes of a row slot (lanes 8k..8k+7).
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);   // row_half_mirror
+    return v;
+}
+// Max / sum over lanes l, l^8, l^16, l^32 (the 8 row slots, same seg).
+__device__ __forceinline__ float max_slots(float v) {
+    v = fmaxf(v, dpp_f<0x128>(v));   // row_ror:8 == xor 8 within 16 lanes
+    v = fmaxf(v, swz_xor16(v));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+__device__ __forceinline__ float sum_slots(float v) {
+    v += dpp_f<0x128>(v);
+    v += swz_xor16(v);
+    v += __shfl_xor(v, 32);
+    return v;
+}
 
-__global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs a) {
+template <bool kFused>
+__global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a) {
     __shared__ float o_sh[kWaves][kGroup][kHeadDim];
     __shared__ float ml_sh[kWaves][kGroup][2];
-    __shared__ float ms_sh[kGroup][kMaxMergeSplits];
-    __shared__ float ls_sh[kGroup][kMaxMergeSplits];
-    __shared__ uint32_t last_sh;
+    __shared__ uint16_t qn_sh[kGroup][kHeadDim];
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int seg = lane & 7;              // dims [16*seg, 16*seg+16)
     const int slot = lane >> 3;            // row within a round
-    const uint32_t g = blockIdx.y;
-    const uint32_t split = blockIdx.x;
-    const uint32_t row0 = split * a.split_len;
-    const uint32_t row_end = min(row0 + a.split_len, a.n_keys);
-    const float c2 = a.scale * 1.4426950408889634f;   // scores in log2 units
+    // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
+    // linear id, so ids are laid out as [split / 8][g][split % 8] — the KV
+    // heads of one split share an XCD and hence its L2 copy of the rows' FP32
+    // scale lines (one 128-byte line holds the scales of all heads of a row).
+    const uint32_t nkv = gridDim.x / ((a.n_splits + 7) / 8 * 8);
+    const uint32_t within = blockIdx.x % (8 * nkv);
+    const uint32_t g = within / 8;
+    const uint32_t split = blockIdx.x / (8 * nkv) * 8 + within % 8;
+    if (split >= a.n_splits) return;
+    const uint32_t row0 = min(split * a.split_len, a.n_rows);
+    const uint32_t row_end = min(row0 + a.split_len, a.n_rows);
+    const float c2 = a.scale * kLog2e;   // scores in log2 units
 
-    // Query slice of the 4 heads, and its per-lane sums (for the +128 bias).
-    float qf[kGroup][16], qsum[kGroup];
+    const uint64_t kv_dim = a.kv_dim;
+    const uint32_t nb_row = a.kv_dim / kBlock;
+    const uint32_t col = g * kHeadDim + 16 * seg;
+    const uint32_t dcol = g * (kHeadDim / kBlock) + (seg >> 1);
+    auto row_of = [&](uint32_t b, int r) {
+        return row0 + 32u * (kRounds * b + r) + 8u * wave + slot;
+    };
+    auto load = [&](Batch& B, uint32_t b) {
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const uint64_t row = min(row_of(b, r), row_end - 1);
+            B.kq[r] = *reinterpret_cast<const Q16*>(a.k.qs + row * kv_dim + col);
+            B.kd[r] = a.k.d[row * nb_row + dcol];
+            B.vq[r] = *reinterpret_cast<const Q16*>(a.v.qs + row * kv_dim + col);
+            B.vd[r] = a.v.d[row * nb_row + dcol];
+        }
+    };
+    const uint32_t n_rows = row_end - row0;
+    const uint32_t n_batches =
+        n_rows > 8u * wave ? (n_rows - 8u * wave + 32u * kRounds - 1) / (32u * kRounds) : 0u;
+    Batch A, Bb;
+    if (n_batches > 0) load(A, 0);   // first loads in flight before the query is read
+
+    // ---- the query slice of the 4 heads (as f16 pairs) ---------------------
+    const uint16_t* qsrc;
+    if constexpr (kFused) {
+        // q_norm_rope for head 4g + wave (q_norm_rope_fused.wgsl:38-96), into LDS.
+        const uint32_t h = g * kGroup + wave;
+        const uint16_t* qr = a.q + static_cast<uint64_t>(h) * kHeadDim;
+        const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos) * kHeadDim + 2 * lane;
+        float o0, o1;
+        norm_rope_pair(h2f(qr[lane]), h2f(qr[lane + 64]), h2f(a.w_norms[a.w_q_off + lane]),
+                       h2f(a.w_norms[a.w_q_off + lane + 64]), h2f(cs[0]), h2f(cs[1]), a.eps, o0, o1);
+        qn_sh[wave][lane] = f2h(o0);
+        qn_sh[wave][lane + 64] = f2h(o1);
+        if (split == 0) {
+            a.q_norm[h * kHeadDim + lane] = f2h(o0);
+            a.q_norm[h * kHeadDim + lane + 64] = f2h(o1);
+        }
+        if (split == a.n_splits - 1 && wave < 2) {
+            // kv_writeback of row `pos` for KV head g (kv_writeback_fused.wgsl):
+            // wave 0 writes K (norm + RoPE + Q8_0), wave 1 writes V (Q8_0).
+            const uint64_t d_idx = static_cast<uint64_t>(a.pos) * nb_row + g * (kHeadDim / kBlock);
+            const uint64_t qs_idx = static_cast<uint64_t>(a.pos) * kv_dim + g * kHeadDim;
+            const uint16_t* src = (wave == 0 ? a.k_cur : a.v_cur) + g * kHeadDim;
+            float x0 = h2f(src[lane]), x1 = h2f(src[lane + 64]);
+            if (wave == 0) {
+                norm_rope_pair(x0, x1, h2f(a.w_norms[a.w_k_off + lane]), h2f(a.w_norms[a.w_k_off + lane + 64]),
+                               h2f(cs[0]), h2f(cs[1]), a.eps, x0, x1);
+                quantize_store_pair(x0, x1, lane, const_cast<float*>(a.k.d) + d_idx,
+                                    const_cast<int8_t*>(a.k.qs) + qs_idx);
+            } else {
+                quantize_store_pair(x0, x1, lane, const_cast<float*>(a.v.d) + d_idx,
+                                    const_cast<int8_t*>(a.v.qs) + qs_idx);
+            }
+        }
+        __syncthreads();
+        qsrc = &qn_sh[0][0];
+    } else {
+        qsrc = a.q + static_cast<uint64_t>(g) * kGroup * kHeadDim;
+    }
+    h2 qh[kGroup][8];
+    float qbias[kGroup];   // -1152 * sum(q) over this lane's 16 dims
 #pragma unroll
     for (int h = 0; h < kGroup; h++) {
-        const uint16_t* qp = a.q + (static_cast<uint64_t>(g) * kGroup + h) * kHeadDim + 16 * seg;
+        const uint16_t* qp = qsrc + h * kHeadDim + 16 * seg;
         const Q16 r0 = *reinterpret_cast<const Q16*>(qp);
         const Q16 r1 = *reinterpret_cast<const Q16*>(qp + 8);
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            qf[h][2 * i] = h2f(r0.w[i] & 0xffffu);
-            qf[h][2 * i + 1] = h2f(r0.w[i] >> 16);
-            qf[h][8 + 2 * i] = h2f(r1.w[i] & 0xffffu);
-            qf[h][8 + 2 * i + 1] = h2f(r1.w[i] >> 16);
+            qh[h][i] = __builtin_bit_cast(h2, r0.w[i]);
+            qh[h][4 + i] = __builtin_bit_cast(h2, r1.w[i]);
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) s += qf[h][i];
-        qsum[h] = 128.0f * s;
+        for (int i = 0; i < 8; i++) s += static_cast<float>(qh[h][i].x) + static_cast<float>(qh[h][i].y);
+        qbias[h] = -1152.0f * s;
     }
 
     float o[kGroup][16], bsum[kGroup], lsum[kGroup], m_run[kGroup];
@@ -93,47 +201,26 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs a) {
         for (int i = 0; i < 16; i++) o[h][i] = 0.0f;
     }
 
-    const uint64_t kv_dim = a.kv_dim;
-    const uint32_t nb_row = a.kv_dim / kBlock;
-    const uint32_t col = g * kHeadDim + 16 * seg;
-    const uint32_t dcol = g * (kHeadDim / kBlock) + (seg >> 1);
-    // Row of (batch b, round r) for this lane: row0 + 32*(kRounds*b + r) + 8*wave + slot.
-    auto row_of = [&](uint32_t b, int r) {
-        return row0 + 32u * (kRounds * b + r) + 8u * wave + slot;
-    };
-    auto load = [&](Batch& B, uint32_t b) {
-#pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            const uint32_t row = row_of(b, r);
-            const bool ok = row < row_end;
-            B.kq[r] = ok ? *reinterpret_cast<const Q16*>(a.k.qs + row * kv_dim + col) : Q16{{0, 0, 0, 0}};
-            B.kd[r] = ok ? a.k.d[static_cast<uint64_t>(row) * nb_row + dcol] : 0.0f;
-            B.vq[r] = ok ? *reinterpret_cast<const Q16*>(a.v.qs + row * kv_dim + col) : Q16{{0, 0, 0, 0}};
-            B.vd[r] = ok ? a.v.d[static_cast<uint64_t>(row) * nb_row + dcol] : 0.0f;
-        }
-    };
     auto consume = [&](const Batch& B, uint32_t b) {
         float s[kRounds][kGroup];
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
-            Q16 k;
+            h2 kh[8];
 #pragma unroll
-            for (int i = 0; i < 4; i++) k.w[i] = B.kq[r].w[i] ^ 0x80808080u;
-            float dot[kGroup];
-#pragma unroll
-            for (int h = 0; h < kGroup; h++) {
-                float acc = -qsum[h];
-#pragma unroll
-                for (int i = 0; i < 16; i++) acc = __builtin_fmaf(qf[h][i], ub(k.w[i >> 2], i & 3), acc);
-                dot[h] = acc * B.kd[r];
+            for (int i = 0; i < 4; i++) {
+                const uint32_t x = B.kq[r].w[i] ^ 0x80808080u;
+                kh[2 * i] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kExp64, x, 0x04010400u));
+                kh[2 * i + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kExp64, x, 0x04030402u));
             }
-#pragma unroll
-            for (int off = 1; off <= 4; off <<= 1)
-#pragma unroll
-                for (int h = 0; h < kGroup; h++) dot[h] += __shfl_xor(dot[h], off);
             const bool ok = row_of(b, r) < row_end;
 #pragma unroll
-            for (int h = 0; h < kGroup; h++) s[r][h] = ok ? dot[h] * c2 : -INFINITY;
+            for (int h = 0; h < kGroup; h++) {
+                float acc = qbias[h];
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc = __builtin_amdgcn_fdot2(qh[h][i], kh[i], acc, false);
+                const float dot = sum8(acc * B.kd[r]);
+                s[r][h] = ok ? dot * c2 : -INFINITY;
+            }
         }
         float alpha[kGroup];
         bool moved = false;
@@ -142,9 +229,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs a) {
             float bm = s[0][h];
 #pragma unroll
             for (int r = 1; r < kRounds; r++) bm = fmaxf(bm, s[r][h]);
-            bm = fmaxf(bm, __shfl_xor(bm, 8));
-            bm = fmaxf(bm, __shfl_xor(bm, 16));
-            bm = fmaxf(bm, __shfl_xor(bm, 32));
+            bm = max_slots(bm);
             const float m_new = fmaxf(m_run[h], bm);
             alpha[h] = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 on the first batch
             moved |= m_new != m_run[h];
@@ -161,15 +246,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
-            Q16 v;
-#pragma unroll
-            for (int i = 0; i < 4; i++) v.w[i] = B.vq[r].w[i] ^ 0x80808080u;
             float vf[16];
 #pragma unroll
-            for (int i = 0; i < 16; i++) vf[i] = ub(v.w[i >> 2], i & 3);
+            for (int i = 0; i < 16; i++) vf[i] = ub(B.vq[r].w[i >> 2] ^ 0x80808080u, i & 3);
 #pragma unroll
             for (int h = 0; h < kGroup; h++) {
-                const float p = __builtin_amdgcn_exp2f(s[r][h] - m_run[h]);   // 0 for masked rows
+                // 0 for masked rows, which repeat a real, finite row: p * v stays 0
+                const float p = __builtin_amdgcn_exp2f(s[r][h] - m_run[h]);
                 lsum[h] += p;
                 const float pv = p * B.vd[r];
                 bsum[h] += pv;
@@ -179,12 +262,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs a) {
         }
     };
 
-    // Batches this wave has rows in: rows of batch b start at row_of(b, 0) (slot 0).
-    const uint32_t n_rows = row_end - row0;
-    const uint32_t n_batches = n_rows > 8u * wave ? (n_rows - 8u * wave + 32u * kRounds - 1) / (32u * kRounds) : 0u;
     if (n_batches > 0) {
-        Batch A, Bb;
-        load(A, 0);
         uint32_t b = 0;
         while (true) {
             if (b + 1 < n_batches) load(Bb, b + 1);
@@ -196,17 +274,12 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs a) {
         }
     }
 
-    // ---- per-wave totals: O over the 8 row slots, l over row slots ----------
+    // ---- per-wave totals: O and l over the 8 row slots ---------------------
 #pragma unroll
     for (int h = 0; h < kGroup; h++) {
+        lsum[h] = sum_slots(lsum[h]);
 #pragma unroll
-        for (int i = 0; i < 16; i++) o[h][i] -= 128.0f * bsum[h];
-#pragma unroll
-        for (int off = 8; off <= 32; off <<= 1) {
-            lsum[h] += __shfl_xor(lsum[h], off);
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[h][i] += __shfl_xor(o[h][i], off);
-        }
+        for (int i = 0; i < 16; i++) o[h][i] = sum_slots(o[h][i] - 128.0f * bsum[h]);
     }
     if (slot == 0) {
 #pragma unroll
@@ -234,94 +307,126 @@ __global__ __launch_bounds__(kThreads, 2) void decode_kernel(DecodeArgs a) {
         o0 = __builtin_fmaf(e, o_sh[w][fh][fd], o0);
         o1 = __builtin_fmaf(e, o_sh[w][fh][fd + 1], o1);
     }
-    const uint32_t qh = g * kGroup + fh;
-    uint32_t* out = reinterpret_cast<uint32_t*>(a.out + static_cast<uint64_t>(qh) * kHeadDim + fd);
-    if (a.n_splits == 1) {
+    const uint32_t qhd = g * kGroup + fh;
+    if (!kFused && a.n_splits == 1) {
         const float inv_l = 1.0f / L;
+        uint32_t* out = reinterpret_cast<uint32_t*>(a.out + static_cast<uint64_t>(qhd) * kHeadDim + fd);
         *out = static_cast<uint32_t>(f2h(o0 * inv_l)) | (static_cast<uint32_t>(f2h(o1 * inv_l)) << 16);
         return;
     }
-    float* part = a.partials + (static_cast<uint64_t>(qh) * a.n_splits + split) * kPartStride;
+    float* part = a.partials + (static_cast<uint64_t>(qhd) * a.n_splits + split) * kPartStride;
     *reinterpret_cast<float2*>(part + fd) = make_float2(o0, o1);
-    if ((t & 63) == 0) { part[kHeadDim] = M; part[kHeadDim + 1] = L; }
+    if ((t & 63) == 0) *reinterpret_cast<float2*>(part + kHeadDim) = make_float2(M, L);
+}
 
-    // ---- the last workgroup of this KV head merges all splits --------------
-    __threadfence();
-    __syncthreads();
-    if (t == 0) last_sh = atomicAdd(&a.tickets[g], 1u) == a.n_splits - 1 ? 1u : 0u;
-    __syncthreads();
-    if (last_sh == 0) return;
-    __threadfence();
+// One wave per (query head, 32-dim chunk).
+template <bool kFused>
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
+    const int lane = threadIdx.x;
+    const uint32_t h = blockIdx.x >> 2, c = blockIdx.x & 3;
+    const uint32_t g = h / kGroup;
     const uint32_t ns = a.n_splits;
-    const float* pg = a.partials + static_cast<uint64_t>(g) * kGroup * ns * kPartStride;
-    for (uint32_t i = t; i < kGroup * ns; i += kThreads) {
-        const uint32_t h = i / ns, s = i % ns;
-        const float* ps = pg + (static_cast<uint64_t>(h) * ns + s) * kPartStride;
-        ms_sh[h][s] = __builtin_nontemporal_load(ps + kHeadDim);
-        ls_sh[h][s] = __builtin_nontemporal_load(ps + kHeadDim + 1);
-    }
-    __syncthreads();
-    {   // wave h: global max and weights of head h
-        float mx = -INFINITY;
-        for (uint32_t s = lane; s < ns; s += 64) mx = fmaxf(mx, ms_sh[wave][s]);
-        mx = wave_max(mx);
-        float l = 0.0f;
-        for (uint32_t s = lane; s < ns; s += 64) {
-            const float w = __builtin_amdgcn_exp2f(ms_sh[wave][s] - mx);
-            ms_sh[wave][s] = w;
-            l = __builtin_fmaf(w, ls_sh[wave][s], l);
-        }
-        l = wave_sum(l);
-        if (lane == 0) ls_sh[wave][0] = l;   // slot 0 reused for the total (read after the barrier)
-    }
-    __syncthreads();
-    const float* ph = pg + static_cast<uint64_t>(fh) * ns * kPartStride + fd;
-    float a0 = 0.0f, a1 = 0.0f;
-    uint32_t s = 0;
-    for (; s + 4 <= ns; s += 4) {
-        float2 v[4];
+    const float* ph = a.partials + static_cast<uint64_t>(h) * ns * kPartStride;
+    const float c2 = a.scale * kLog2e;
+
+    // O chunk loads: lane -> splits (lane >> 3) + 8i, dims 32c + 4 (lane & 7) .. +3.
+    const int f4 = lane & 7;
+    float4 ov[kMaxSplits / 8];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            v[j].x = __builtin_nontemporal_load(ph + (s + j) * kPartStride);
-            v[j].y = __builtin_nontemporal_load(ph + (s + j) * kPartStride + 1);
-        }
+    for (int i = 0; i < kMaxSplits / 8; i++) {
+        const uint32_t s = min(static_cast<uint32_t>((lane >> 3) + 8 * i), ns - 1);
+        ov[i] = *reinterpret_cast<const float4*>(ph + static_cast<uint64_t>(s) * kPartStride + 32 * c + 4 * f4);
+    }
+    const uint32_t ls = min(static_cast<uint32_t>(lane), ns - 1);
+    const float2 ml = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls) * kPartStride + kHeadDim);
+    const float m_s = static_cast<uint32_t>(lane) < ns ? ml.x : -INFINITY;
+
+    float s_new = -INFINITY;   // log2-domain score of the new row (fused step)
+    if constexpr (kFused) {
+        const uint16_t* qn = a.q_norm + static_cast<uint64_t>(h) * kHeadDim;
+        const float q0 = h2f(qn[lane]), q1 = h2f(qn[lane + 64]);
+        const uint64_t row = a.pos;
+        const uint32_t nb_row = a.kv_dim / kBlock;
+        const float* kd = a.k.d + row * nb_row + g * (kHeadDim / kBlock);
+        const int8_t* kq = a.k.qs + row * a.kv_dim + g * kHeadDim;
+        const float k0 = kd[lane >> 5] * static_cast<float>(kq[lane]);
+        const float k1 = kd[2 + (lane >> 5)] * static_cast<float>(kq[lane + 64]);
+        s_new = wave_sum(q0 * k0 + q1 * k1) * c2;
+        if (lane < 32) a.q_act[h * kHeadDim + 32 * c + lane] = qn[32 * c + lane];   // q_norm_rope output
+    }
+    const float M = fmaxf(wave_max(m_s), s_new);
+    const float w = m_s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s - M);
+    const float w_new = kFused ? __builtin_amdgcn_exp2f(s_new - M) : 0.0f;
+    const float L = wave_sum(w * (static_cast<uint32_t>(lane) < ns ? ml.y : 0.0f)) + w_new;
+
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float w = ms_sh[fh][s + j];
-            a0 = __builtin_fmaf(w, v[j].x, a0);
-            a1 = __builtin_fmaf(w, v[j].y, a1);
+    for (int i = 0; i < kMaxSplits / 8; i++) {
+        const float wi = __shfl(w, (lane >> 3) + 8 * i);   // 0 for splits >= ns
+        acc.x = __builtin_fmaf(wi, ov[i].x, acc.x);
+        acc.y = __builtin_fmaf(wi, ov[i].y, acc.y);
+        acc.z = __builtin_fmaf(wi, ov[i].z, acc.z);
+        acc.w = __builtin_fmaf(wi, ov[i].w, acc.w);
+    }
+    acc.x = sum_slots(acc.x);
+    acc.y = sum_slots(acc.y);
+    acc.z = sum_slots(acc.z);
+    acc.w = sum_slots(acc.w);
+    if (lane < 8) {
+        const uint32_t d0 = 32 * c + 4 * f4;
+        if constexpr (kFused) {
+            const uint64_t row = a.pos;
+            const uint32_t nb_row = a.kv_dim / kBlock;
+            const float vd = a.v.d[row * nb_row + g * (kHeadDim / kBlock) + (d0 >> 5)];
+            const int8_t* vq = a.v.qs + row * a.kv_dim + g * kHeadDim + d0;
+            acc.x = __builtin_fmaf(w_new, vd * static_cast<float>(vq[0]), acc.x);
+            acc.y = __builtin_fmaf(w_new, vd * static_cast<float>(vq[1]), acc.y);
+            acc.z = __builtin_fmaf(w_new, vd * static_cast<float>(vq[2]), acc.z);
+            acc.w = __builtin_fmaf(w_new, vd * static_cast<float>(vq[3]), acc.w);
         }
+        const float inv_l = 1.0f / L;
+        uint2 o;
+        o.x = static_cast<uint32_t>(f2h(acc.x * inv_l)) | (static_cast<uint32_t>(f2h(acc.y * inv_l)) << 16);
+        o.y = static_cast<uint32_t>(f2h(acc.z * inv_l)) | (static_cast<uint32_t>(f2h(acc.w * inv_l)) << 16);
+        *reinterpret_cast<uint2*>(a.out + static_cast<uint64_t>(h) * kHeadDim + d0) = o;
     }
-    for (; s < ns; s++) {
-        const float w = ms_sh[fh][s];
-        a0 = __builtin_fmaf(w, __builtin_nontemporal_load(ph + s * kPartStride), a0);
-        a1 = __builtin_fmaf(w, __builtin_nontemporal_load(ph + s * kPartStride + 1), a1);
-    }
-    const float inv_l = 1.0f / ls_sh[fh][0];
-    *out = static_cast<uint32_t>(f2h(a0 * inv_l)) | (static_cast<uint32_t>(f2h(a1 * inv_l)) << 16);
-    if (t == 0) atomicExch(&a.tickets[g], 0u);
 }
 
 }  // namespace
 
-void decode_plan(uint32_t n_keys, uint32_t n_kv_head, int cu_count, uint32_t* split_len,
-                 uint32_t* n_splits) {
-    // ~2 workgroups per CU; rows per split a multiple of 32 (one round of all
-    // 4 waves), at least 64, and at most kMaxMergeSplits splits.
+void decode_plan(uint32_t n_rows, uint32_t n_kv_head, int cu_count, uint32_t min_split_rows,
+                 uint32_t* split_len, uint32_t* n_splits) {
+    // Enough workgroups to cover the CUs twice, but at least min_split_rows
+    // rows each (fewer partials at short context) and at most kMaxSplits
+    // splits; rows per split are a multiple of 32 (one round of all 4 waves).
     const uint32_t target = static_cast<uint32_t>(cu_count > 0 ? cu_count : 256) * 2;
     uint32_t want = (target + n_kv_head - 1) / n_kv_head;
     if (want < 1) want = 1;
-    uint32_t len = (n_keys + want - 1) / want;
+    if (want > kMaxSplits) want = kMaxSplits;
+    uint32_t len = (n_rows + want - 1) / want;
+    if (len < min_split_rows) len = min_split_rows;
     len = (len + 31) / 32 * 32;
-    if (len < 64) len = 64;
-    const uint32_t min_len = (n_keys + kMaxMergeSplits - 1) / kMaxMergeSplits;
-    if (len < min_len) len = (min_len + 31) / 32 * 32;
     *split_len = len;
-    *n_splits = (n_keys + len - 1) / len;
+    *n_splits = n_rows == 0 ? 1 : (n_rows + len - 1) / len;
+}
+
+uint32_t decode_max_splits() { return kMaxSplits; }
+uint32_t decode_partial_stride() { return kPartStride; }
+
+static dim3 split_grid(const DecodeArgs& a, uint32_t n_kv_head) {
+    return dim3((a.n_splits + 7) / 8 * 8 * n_kv_head);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(decode_kernel, dim3(a.n_splits, n_kv_head), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(decode_split_kernel<false>, split_grid(a, n_kv_head), dim3(kThreads), 0, s, a);
+    if (a.n_splits > 1)
+        hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_step(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
+    hipLaunchKernelGGL(decode_split_kernel<true>, split_grid(a, n_kv_head), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -110,15 +110,21 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_kernel(PrefillArgs a) {
     const uint32_t sdcol = g * (kHeadDim / kBlock) + (sseg >> 1);
     U4 kq, vq;
     float kd, vd;
+    // Unconditional loads from a clamped row (a predicated load would become a
+    // branch that drains all outstanding loads); rows past kend are zeroed
+    // through their scale when staged.
+    bool srow_ok = false;
     auto load_chunk = [&](uint32_t c) {
         const uint32_t row = c * kChunk + srow;
-        const bool ok = row < kend;
-        kq = ok ? *reinterpret_cast<const U4*>(a.k.qs + row * kv_dim + scol) : U4{{0, 0, 0, 0}};
-        vq = ok ? *reinterpret_cast<const U4*>(a.v.qs + row * kv_dim + scol) : U4{{0, 0, 0, 0}};
-        kd = ok ? a.k.d[static_cast<uint64_t>(row) * nb_row + sdcol] : 0.0f;
-        vd = ok ? a.v.d[static_cast<uint64_t>(row) * nb_row + sdcol] : 0.0f;
+        srow_ok = row < kend;
+        const uint64_t r = min(row, kend - 1);
+        kq = *reinterpret_cast<const U4*>(a.k.qs + r * kv_dim + scol);
+        vq = *reinterpret_cast<const U4*>(a.v.qs + r * kv_dim + scol);
+        kd = a.k.d[r * nb_row + sdcol];
+        vd = a.v.d[r * nb_row + sdcol];
     };
     auto store_chunk = [&](int buf) {
+        if (!srow_ok) { kd = 0.0f; vd = 0.0f; }
         U4 lo, hi;
 #pragma unroll
         for (int i = 0; i < 4; i++) {

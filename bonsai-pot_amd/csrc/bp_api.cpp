@@ -19,6 +19,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -37,7 +38,8 @@ struct bp_model {
     uint16_t* rope_cs;
     float* partials;
     uint64_t partials_floats;
-    uint32_t* tickets;
+    uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
+    uint32_t decode_min_split_rows;
     bool lost;
     std::string lost_message;
 };
@@ -137,6 +139,22 @@ bp::KvView kv_view(const bp_model* m, const uint8_t* buf, uint32_t il) {
 
 constexpr uint32_t kMaxGridY = 65535;
 
+bp::DecodeArgs decode_args(const bp_model* m, void* act, uint32_t q_off, uint32_t out_off, uint32_t il,
+                           uint32_t n_rows) {
+    bp::DecodeArgs a{};
+    a.q = static_cast<const uint16_t*>(act) + q_off;
+    a.out = static_cast<uint16_t*>(act) + out_off;
+    a.k = kv_view(m, m->kv_k, il);
+    a.v = kv_view(m, m->kv_v, il);
+    a.partials = m->partials;
+    a.kv_dim = m->kv_dim;
+    a.n_rows = n_rows;
+    bp::decode_plan(n_rows, m->cfg.n_kv_head, m->cu_count, m->decode_min_split_rows, &a.split_len,
+                    &a.n_splits);
+    a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:838
+    return a;
+}
+
 }  // namespace
 
 extern "C" {
@@ -217,18 +235,19 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
     m->cu_count = prop.multiProcessorCount;
 
     m->kv_bytes = bp_kv_buffer_bytes(cfg->n_layer, m->kv_dim, max_seq);
-    // Split-K partials: at most ~2 workgroups per CU -> bounded split count;
-    // size for the worst case of the planner over [1, max_seq] rows.
-    uint32_t split_len = 0, n_splits = 0;
-    bp::decode_plan(max_seq, cfg->n_kv_head, m->cu_count, &split_len, &n_splits);
-    const uint64_t max_splits = static_cast<uint64_t>(2 * m->cu_count / cfg->n_kv_head + 2);
-    m->partials_floats = static_cast<uint64_t>(cfg->n_head) * std::max<uint64_t>(max_splits, n_splits) *
-                         (bp::kHeadDim + 2);
+    // Split-K partials: n_head x (at most decode_max_splits()) x stride floats.
+    m->decode_min_split_rows = 256;
+    if (const char* env = std::getenv("BP_DECODE_MIN_SPLIT_ROWS")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 32 && v <= (1 << 20)) m->decode_min_split_rows = static_cast<uint32_t>(v);
+    }
+    m->partials_floats = static_cast<uint64_t>(cfg->n_head) * bp::decode_max_splits() *
+                         bp::decode_partial_stride();
     const size_t rope_elems = static_cast<size_t>(max_seq) * cfg->head_dim;
     if (hipMalloc(&m->kv_k, m->kv_bytes) != hipSuccess || hipMalloc(&m->kv_v, m->kv_bytes) != hipSuccess ||
         hipMalloc(&m->rope_cs, rope_elems * 2) != hipSuccess ||
         hipMalloc(&m->partials, m->partials_floats * 4) != hipSuccess ||
-        hipMalloc(&m->tickets, cfg->n_kv_head * sizeof(uint32_t)) != hipSuccess) {
+        hipMalloc(&m->q_norm, static_cast<size_t>(cfg->n_head) * cfg->head_dim * 2) != hipSuccess) {
         (void)hipGetLastError();
         return bail(fail(BP_ERR_OUT_OF_MEMORY, "hipMalloc failed for KV cache of %llu bytes x2",
                          static_cast<unsigned long long>(m->kv_bytes)));
@@ -238,7 +257,6 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
                         "upload rope table")) != BP_OK ||
         (st = hip_check(m, hipMemset(m->kv_k, 0, m->kv_bytes), "zero kv_k")) != BP_OK ||
         (st = hip_check(m, hipMemset(m->kv_v, 0, m->kv_bytes), "zero kv_v")) != BP_OK ||
-        (st = hip_check(m, hipMemset(m->tickets, 0, cfg->n_kv_head * sizeof(uint32_t)), "zero tickets")) != BP_OK ||
         (st = hip_check(m, hipDeviceSynchronize(), "model create sync")) != BP_OK)
         return bail(st);
     *out = m;
@@ -253,7 +271,7 @@ void bp_model_destroy(bp_model* m) {
         if (m->kv_v) (void)hipFree(m->kv_v);
         if (m->rope_cs) (void)hipFree(m->rope_cs);
         if (m->partials) (void)hipFree(m->partials);
-        if (m->tickets) (void)hipFree(m->tickets);
+        if (m->q_norm) (void)hipFree(m->q_norm);
     }
     (void)hipGetLastError();
     delete m;
@@ -369,22 +387,43 @@ bp_status bp_dispatch_attention_decode(bp_model* m, void* act, uint32_t q_off, u
     if (pos >= m->max_seq)
         return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens 1 > max_seq %u", pos,
                     m->max_seq);
-    if ((q_off & 7u) || (out_off & 1u))
-        return fail(BP_ERR_INVALID_ARG, "q_off must be a multiple of 8 and out_off even (aligned f16 rows)");
-    bp::DecodeArgs a;
-    a.q = static_cast<const uint16_t*>(act) + q_off;
-    a.out = static_cast<uint16_t*>(act) + out_off;
-    a.k = kv_view(m, m->kv_k, layer_il);
-    a.v = kv_view(m, m->kv_v, layer_il);
-    a.partials = m->partials;
-    a.tickets = m->tickets;
-    a.kv_dim = m->kv_dim;
-    a.n_keys = pos + 1;   // src/forward.rs:822 (cur_pos = pos + 1)
-    bp::decode_plan(a.n_keys, m->cfg.n_kv_head, m->cu_count, &a.split_len, &a.n_splits);
-    if (static_cast<uint64_t>(a.n_splits) * m->cfg.n_head * (bp::kHeadDim + 2) > m->partials_floats)
+    if ((q_off & 7u) || (out_off & 3u))
+        return fail(BP_ERR_INVALID_ARG, "q_off must be a multiple of 8 and out_off of 4 (aligned f16 rows)");
+    bp::DecodeArgs a = decode_args(m, act, q_off, out_off, layer_il, pos + 1);   // src/forward.rs:822
+    if (static_cast<uint64_t>(a.n_splits) * m->cfg.n_head * bp::decode_partial_stride() > m->partials_floats)
         return fail(BP_ERR_CONFIG, "internal: partials scratch too small for %u splits", a.n_splits);
-    a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:838
     return hip_check(m, bp::launch_decode(a, m->cfg.n_kv_head, m->stream), "attention_decode launch");
+}
+
+bp_status bp_dispatch_attention_decode_step(bp_model* m, void* act, const void* w_norms, uint32_t q_off,
+                                            uint32_t k_cur_off, uint32_t v_cur_off, uint32_t out_off,
+                                            uint32_t w_q_norm_off, uint32_t w_k_norm_off, uint32_t layer_il,
+                                            uint32_t pos) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act || !w_norms) return fail(BP_ERR_INVALID_ARG, "act/w_norms is NULL");
+    if (layer_il >= m->cfg.n_layer)
+        return fail(BP_ERR_INVALID_ARG, "layer %u >= n_layer %u", layer_il, m->cfg.n_layer);
+    if (pos >= m->max_seq)
+        return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens 1 > max_seq %u", pos,
+                    m->max_seq);
+    if ((out_off & 3u))
+        return fail(BP_ERR_INVALID_ARG, "out_off must be a multiple of 4 (8-byte aligned f16 rows)");
+    // The split pass streams rows [0, pos); row `pos` is written and added in-kernel.
+    bp::DecodeArgs a = decode_args(m, act, q_off, out_off, layer_il, pos);
+    a.q_act = static_cast<uint16_t*>(act) + q_off;
+    a.q_norm = m->q_norm;
+    a.k_cur = static_cast<const uint16_t*>(act) + k_cur_off;
+    a.v_cur = static_cast<const uint16_t*>(act) + v_cur_off;
+    a.w_norms = static_cast<const uint16_t*>(w_norms);
+    a.rope_cs = m->rope_cs;
+    a.w_q_off = w_q_norm_off;
+    a.w_k_off = w_k_norm_off;
+    a.pos = pos;
+    a.eps = m->cfg.rms_eps;
+    if (static_cast<uint64_t>(a.n_splits) * m->cfg.n_head * bp::decode_partial_stride() > m->partials_floats)
+        return fail(BP_ERR_CONFIG, "internal: partials scratch too small for %u splits", a.n_splits);
+    return hip_check(m, bp::launch_decode_step(a, m->cfg.n_kv_head, m->stream), "attention_decode_step launch");
 }
 
 bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t out_off, uint32_t layer_il,

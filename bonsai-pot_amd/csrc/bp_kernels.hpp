@@ -46,16 +46,27 @@ struct KvWritebackArgs {
 };
 
 struct DecodeArgs {
-    const uint16_t* q;        // act + q_off: [n_head][128]
+    const uint16_t* q;        // act + q_off: [n_head][128] (raw, un-normalized q when fused)
     uint16_t* out;            // act + out_off: [n_head][128]
     KvView k, v;              // layer bases
-    float* partials;          // [n_head][n_splits][130]
-    uint32_t* tickets;        // [n_kv_head], zero between launches
+    float* partials;          // [n_head][n_splits][decode_partial_stride()]
     uint32_t kv_dim;
-    uint32_t n_keys;          // rows attended: pos + 1
+    uint32_t n_rows;          // rows streamed by the split pass: [0, n_rows)
     uint32_t split_len;       // rows per workgroup, multiple of 32
-    uint32_t n_splits;
+    uint32_t n_splits;        // >= 1
     float scale;
+    // Fused decode step only (q_norm_rope + kv_writeback of row `pos` + attention
+    // over rows [0, pos]): the split pass normalizes q itself and writes cache row
+    // `pos`; the merge pass adds that row and stores the normalized q into act.
+    uint16_t* q_act;          // act + q_off (receives the normalized q)
+    uint16_t* q_norm;         // scratch [n_head][128] f16
+    const uint16_t* k_cur;    // act + k_cur_off: [n_kv_head][128]
+    const uint16_t* v_cur;    // act + v_cur_off
+    const uint16_t* w_norms;
+    const uint16_t* rope_cs;
+    uint64_t w_q_off, w_k_off;
+    uint32_t pos;
+    float eps;
 };
 
 struct PrefillArgs {
@@ -75,10 +86,16 @@ hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t 
                               hipStream_t s);
 hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uint32_t m_tokens,
                                hipStream_t s);
-// Partial buffer floats needed by a decode over n_keys rows.
-void decode_plan(uint32_t n_keys, uint32_t n_kv_head, int cu_count, uint32_t* split_len,
-                 uint32_t* n_splits);
+// Split-K plan of a decode over n_rows rows (1 <= n_splits <= decode_max_splits()).
+void decode_plan(uint32_t n_rows, uint32_t n_kv_head, int cu_count, uint32_t min_split_rows,
+                 uint32_t* split_len, uint32_t* n_splits);
+uint32_t decode_max_splits();
+uint32_t decode_partial_stride();   // floats per (head, split) partial
+// Plain decode (q already normalized, cache row already written): one launch
+// when n_splits == 1, else split pass + merge pass.
 hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s);
+// Fused decode step: split pass (with q norm + row writeback) + merge pass.
+hipError_t launch_decode_step(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s);
 
 }  // namespace bp

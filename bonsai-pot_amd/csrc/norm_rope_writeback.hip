@@ -13,57 +13,11 @@
 // and the RMSNorm reduction uses the fixed butterfly order
 //   s_j = x_j*x_j + x_{j+64}*x_{j+64};  s += shfl_xor(s, 32, 16, 8, 4, 2, 1)
 // so cache bytes and f16 outputs match the CPU oracle bit for bit.
-#include "bp_device.hpp"
 #include "bp_kernels.hpp"
+#include "bp_norm_rope.hpp"
 
 namespace bp {
 namespace {
-
-// RMSNorm(x) * w followed by NEOX RoPE, for the pair (x0 = x[j], x1 = x[j+64]).
-// q_norm_rope_fused.wgsl:53-93 / kv_writeback_fused.wgsl:69-108.
-__device__ __forceinline__ void norm_rope_pair(float x0, float x1, float w0, float w1, float c,
-                                               float s, float eps, float& o0, float& o1) {
-    float sq = x0 * x0 + x1 * x1;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sq = sq + __shfl_xor(sq, off);
-    float inv_h = 1.0f / sqrtf(sq / 128.0f + eps);
-    float n0 = x0 * inv_h * w0;
-    float n1 = x1 * inv_h * w1;
-    o0 = n0 * c - n1 * s;   // kv_writeback_fused.wgsl:102
-    o1 = n0 * s + n1 * c;   // kv_writeback_fused.wgsl:107
-}
-
-// Q8_0-quantize the pair and store it; lanes 0-31 own blocks 0 and 2, lanes
-// 32-63 blocks 1 and 3 (kv_writeback_fused.wgsl:118-200).
-__device__ __forceinline__ void quantize_store_pair(float x0, float x1, int lane, float* d_row,
-                                                    int8_t* qs_row) {
-    float a0 = fabsf(x0), a1 = fabsf(x1);
-#pragma unroll
-    for (int off = 1; off <= 16; off <<= 1) {
-        a0 = fmaxf(a0, __shfl_xor(a0, off));
-        a1 = fmaxf(a1, __shfl_xor(a1, off));
-    }
-    float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
-    float i0 = d0 > 0.0f ? 1.0f / d0 : 0.0f;
-    float i1 = d1 > 0.0f ? 1.0f / d1 : 0.0f;
-    int q0 = static_cast<int>(fminf(fmaxf(rintf(x0 * i0), -127.0f), 127.0f));
-    int q1 = static_cast<int>(fminf(fmaxf(rintf(x1 * i1), -127.0f), 127.0f));
-    // Gather 4 consecutive lanes' bytes into one little-endian word.
-    uint32_t p = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8);
-    int b = lane & ~3;
-    uint32_t p0 = __shfl(p, b), p1 = __shfl(p, b + 1), p2 = __shfl(p, b + 2), p3 = __shfl(p, b + 3);
-    if ((lane & 3) == 0) {
-        uint32_t lo = (p0 & 0xffu) | ((p1 & 0xffu) << 8) | ((p2 & 0xffu) << 16) | ((p3 & 0xffu) << 24);
-        uint32_t hi = (p0 >> 8) | ((p1 >> 8) << 8) | ((p2 >> 8) << 16) | ((p3 >> 8) << 24);
-        *reinterpret_cast<uint32_t*>(qs_row + lane) = lo;
-        *reinterpret_cast<uint32_t*>(qs_row + 64 + lane) = hi;
-    }
-    if ((lane & 31) == 0) {
-        int blk = lane >> 5;          // 0 or 1
-        d_row[blk] = d0;              // elements [32*blk, 32*blk+32)
-        d_row[blk + 2] = d1;          // elements [64+32*blk, ...)
-    }
-}
 
 __global__ __launch_bounds__(64) void q_norm_rope_kernel(QNormRopeArgs a) {
     const int j = threadIdx.x;

@@ -10,6 +10,7 @@
  *   bp_dispatch_kv_writeback_fused   <- dispatch_kv_writeback_fused  src/forward.rs:359-388
  *   bp_dispatch_attention_decode     <- split+merge block in layer_post_kv_in_pass
  *                                       src/forward.rs:820-857
+ *   bp_dispatch_attention_decode_step <- the three above for one token (fused, 2 launches)
  *   bp_dispatch_attention            <- dispatch_attention           src/forward.rs:501-532
  *   bp_model_create / _destroy       <- KV / RoPE / partials part of Model::load_with_options
  *                                       src/model.rs:1148-1248
@@ -110,6 +111,19 @@ bp_status bp_dispatch_kv_writeback_fused(bp_model* model, const void* act, const
  * log-sum-exp merge; writes f16 [n_head][128] at act[out_off]. */
 bp_status bp_dispatch_attention_decode(bp_model* model, void* act, uint32_t q_off,
                                        uint32_t out_off, uint32_t layer_il, uint32_t pos);
+
+/* One whole attention decode step for one layer at step position `pos`, in
+ * two launches instead of the reference's four dispatches: the same results as
+ *   bp_dispatch_q_norm_rope_fused(act, w_norms, q_off, w_q_norm_off, pos, 1)
+ *   bp_dispatch_kv_writeback_fused(act, w_norms, k_cur_off, v_cur_off, w_k_norm_off, layer_il, pos, 1)
+ *   bp_dispatch_attention_decode(act, q_off, out_off, layer_il, pos)
+ * i.e. src/forward.rs:796-804 + :618-628 + :820-857 for one token. act[q_off]
+ * holds the raw (pre-norm) query and receives the normalized one; cache row
+ * `pos` receives the new K/V; act[out_off] receives the attention output. */
+bp_status bp_dispatch_attention_decode_step(bp_model* model, void* act, const void* w_norms,
+                                            uint32_t q_off, uint32_t k_cur_off, uint32_t v_cur_off,
+                                            uint32_t out_off, uint32_t w_q_norm_off,
+                                            uint32_t w_k_norm_off, uint32_t layer_il, uint32_t pos);
 
 /* Batched attention (src/shaders/attention.wgsl, src/forward.rs:501-532) over
  * m_tokens query tokens at act[q_off] ([m][n_head][128] f16), writing

@@ -166,6 +166,13 @@ class DeviceScenario:
         sc = self.sc
         self.model.dispatch_attention_decode(self.act.data_ptr(), sc.q_off, sc.out_off, il, pos)
 
+    def decode_step(self, il, pos):
+        """Fused q_norm_rope + kv_writeback + decode attention for token 0 of the scenario."""
+        sc = self.sc
+        self.model.dispatch_attention_decode_step(self.act.data_ptr(), self.w.data_ptr(), sc.q_off,
+                                                  sc.k_off, sc.v_off, sc.out_off, sc.w_q_off,
+                                                  sc.w_k_off, il, pos)
+
     def out_f32(self, m=None) -> np.ndarray:
         sc = self.sc
         m = sc.m if m is None else m

@@ -159,3 +159,76 @@ def test_prefill_full_size_sampled_rows(cuda, m, pos_base):
     want = sc.oracle_attention(0, pos_base, is_prefill=True, tokens=tokens)
     got = dev.out_f32()[tokens]
     assert_attn_close(got, want, f"prefill m={m} pos_base={pos_base}")
+
+
+def test_decode_repeated_calls_fresh_partials(cuda):
+    """Back-to-back decodes on one model (different layers, positions and queries)
+    reuse the split-K scratch and tickets; every output must match its own oracle
+    result, so stale partials from an earlier launch would show up here."""
+    _say("[decode] repeated calls")
+    cfg = layout.Config(n_layer=3)
+    max_seq = 6000
+    sc = Scenario(cfg, max_seq=max_seq, m_tokens=1, seed=61)
+    for il in range(3):
+        pre = Scenario(cfg, max_seq, 5000, seed=62 + il, with_q=False)
+        pre.kv_k, pre.kv_v = sc.kv_k, sc.kv_v
+        pre.oracle_writeback(il, 0)
+    dev = DeviceScenario(sc, upload_kv=True)
+    rng = np.random.default_rng(5)
+    for step, (il, pos) in enumerate([(0, 4999), (1, 3000), (2, 4095), (0, 700), (1, 4999), (2, 64)]):
+        q = rng.standard_normal(cfg.q_dim).astype(np.float16).view(np.uint16)
+        sc.act[sc.q_off:sc.q_off + cfg.q_dim] = q
+        dev.act[sc.q_off:sc.q_off + cfg.q_dim] = __import__("torch").from_numpy(q.view(np.int16).copy()).cuda()
+        dev.decode(il, pos)
+        _, want = sc.oracle_decode(il, pos)
+        assert_attn_close(dev.out_f32(1)[0], want, f"repeat step {step} layer {il} pos {pos}")
+
+
+@pytest.mark.parametrize("pos,w_std", [(0, 0.0), (1, 0.1), (40, 0.1), (4096, 0.0), (32768, 0.1)])
+def test_fused_decode_step(cuda, pos, w_std):
+    """bp_dispatch_attention_decode_step == q_norm_rope + kv_writeback + decode:
+    normalized q and cache bytes bit-exact, attention output within tolerance."""
+    _say(f"[decode-step] pos={pos}")
+    cfg = layout.Config(n_layer=2)
+    sc = Scenario(cfg, max_seq=pos + 4, m_tokens=1, seed=700 + pos, w_std=w_std)
+    _prefill_cache(sc, 1, pos, seed=800 + pos)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.decode_step(1, pos)
+    sc.oracle_q_norm_rope(pos)
+    sc.oracle_writeback(1, pos)
+    k, v = dev.kv_host()
+    assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v), "cache bytes differ"
+    act = dev.act_host()
+    assert np.array_equal(act[:cfg.q_dim], sc.act[:cfg.q_dim]), "normalized q differs"
+    _, want = sc.oracle_decode(1, pos)
+    assert_attn_close(dev.out_f32(1)[0], want, f"decode step pos={pos}")
+
+
+def test_fused_decode_step_sequence(cuda):
+    """Eight consecutive fused steps (pos 300..307) across two layers on one model:
+    each step's row is then attended by the next; matches the oracle every step."""
+    _say("[decode-step] sequence")
+    cfg = layout.Config(n_layer=2)
+    sc = Scenario(cfg, max_seq=320, m_tokens=1, seed=91)
+    _prefill_cache(sc, 0, 300, seed=92)
+    pre1 = Scenario(cfg, 320, 300, seed=93, with_q=False)
+    pre1.kv_k, pre1.kv_v = sc.kv_k, sc.kv_v
+    pre1.oracle_writeback(1, 0)
+    dev = DeviceScenario(sc, upload_kv=True)
+    import torch
+    rng = np.random.default_rng(9)
+    for step in range(8):
+        pos = 300 + step
+        raw = rng.standard_normal(cfg.q_dim + 2 * cfg.kv_dim).astype(np.float16).view(np.uint16)
+        sc.act[:raw.size] = raw
+        dev.act[:raw.size] = torch.from_numpy(raw.view(np.int16).copy()).cuda()
+        for il in (0, 1):
+            sc.act[:raw.size] = raw
+            dev.act[:raw.size] = torch.from_numpy(raw.view(np.int16).copy()).cuda()
+            dev.decode_step(il, pos)
+            sc.oracle_q_norm_rope(pos)
+            sc.oracle_writeback(il, pos)
+            _, want = sc.oracle_decode(il, pos)
+            assert_attn_close(dev.out_f32(1)[0], want, f"step {step} layer {il}")
+    k, v = dev.kv_host()
+    assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v)

@@ -11,7 +11,8 @@ from .errors import BP_OK, error_for
 from .layout import Config
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-library_path = os.path.join(os.path.dirname(_HERE), "lib", "libbonsai_pot_hip.so")
+library_path = os.environ.get("BONSAI_POT_HIP_LIB") or os.path.join(os.path.dirname(_HERE), "lib",
+                                                                   "libbonsai_pot_hip.so")
 
 if not os.path.exists(library_path):
     raise ImportError(

@@ -4,19 +4,24 @@
 // attends rows [0, cur) with cur = causal ? pos + m + 1 : pos, f32 softmax,
 // f16 output — computed as a flash-attention over LDS tiles:
 //
-//  * grid = (n_tiles, n_kv_head); a 512-thread workgroup owns one KV head and
-//    64 query tokens. Wave w owns tokens [16 (w & 3), +16) of the tile for the
-//    GQA head pair w >> 2 (heads 2(w>>2), +1), so every K/V chunk staged in LDS
-//    serves 4 x 64 query rows, and 2 waves per SIMD let one wave's softmax
-//    overlap the other's MFMAs. Tiles are issued heaviest first.
-//  * K/V are consumed in chunks of 32 rows. Staging dequantizes Q8_0 to f16
-//    (d * q, one rounding) into double-buffered LDS — K row-major, V
-//    transposed (dim-major) so both MFMA operands are single 16-byte reads —
-//    with a register prefetch distance of two chunks.
+//  * Query tokens form tiles of 32. A 512-thread workgroup owns one KV head
+//    and a zig-zag PAIR of tiles (p, n_tiles-1-p): waves 0-3 take tile p,
+//    waves 4-7 tile n_tiles-1-p, each wave 16 tokens x 2 GQA heads. Under the
+//    causal mask the two tiles' work sums to the same amount for every pair,
+//    so the 256 CUs finish together, and each SIMD holds one wave of each tile
+//    (one's softmax overlaps the other's MFMAs). Both tiles read the same cache
+//    rows (the light tile's range is a prefix of the heavy one's), so every
+//    chunk is staged once.
+//  * K/V are consumed in chunks of 64 rows. Every thread stages 16 bytes of K
+//    and 2 x 8 bytes of V per chunk (register prefetch distance of two
+//    chunks), dequantizing Q8_0 to f16 (d * q, one rounding) into
+//    double-buffered LDS: K row-major, V transposed (dim-major, 16-byte groups
+//    XOR-swizzled by row to spread the transposed writes over the banks), so
+//    both MFMA operands are single 16-byte LDS reads.
 //  * S^T = K Q^T with v_mfma_f32_16x16x32_f16 (K = 32 dims per step): the
-//    output fragment of lane l holds 8 keys of token (l % 16). With the keys
-//    of a chunk stored in V^T in the matching permuted order, that fragment
-//    is directly the B operand of O^T = V^T P^T — no shuffles, no LDS trip.
+//    output fragment of lane l holds 8 keys of token (l % 16) per 32 keys. With
+//    the keys stored in V^T in the matching permuted order, those fragments are
+//    directly the B operand of O^T = V^T P^T — no shuffles, no LDS trip.
 //  * Online softmax in the exp2 domain (scale * log2 e folded into one
 //    multiply), row max across the 4 lane groups by swizzle/permute, and a
 //    lazy running max (moved only by more than kLazy log2 units), so the O
@@ -37,8 +42,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 512;
 constexpr int kHeadsPerWave = 2;
-constexpr int kTileTok = 64;             // query tokens per workgroup
-constexpr int kChunk = 32;               // cache rows per LDS chunk
+constexpr int kChunk = 64;               // cache rows per LDS chunk
+constexpr int kSub = kChunk / 16;        // 16-row S^T sub-tiles per chunk
 constexpr int kKStride = kHeadDim + 8;   // halves per K row in LDS (pad vs bank conflicts)
 constexpr int kVStride = kChunk + 8;     // halves per V^T row in LDS
 constexpr float kLazy = 8.0f;            // lazy-rescale threshold (log2 units)
@@ -49,11 +54,18 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Position of chunk row `key` (0..31) along the MFMA k axis of the PV step:
-// lane group g holds S^T rows {4g..4g+3} (sub-tile 0) and {16+4g..16+4g+3}
-// (sub-tile 1), which become its k slots 8g..8g+3 and 8g+4..8g+7.
+// Position of chunk row `key` (0..63) along the MFMA k axis of the PV step:
+// per 32 keys, lane group g holds S^T rows {4g..4g+3} (first sub-tile) and
+// {16+4g..16+4g+3} (second), which become its k slots 8g..8g+3, 8g+4..8g+7.
 __device__ __forceinline__ int v_slot(int key) {
-    return key < 16 ? 8 * (key >> 2) + (key & 3) : 8 * ((key - 16) >> 2) + 4 + (key & 3);
+    const int k = key & 31;
+    const int s = k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3);
+    return (key & 32) + s;
+}
+// Half-word offset of (V^T row, slot) in LDS: 16-byte group (slot >> 3) is
+// XOR-swizzled with (row >> 3) & 7.
+__device__ __forceinline__ int v_addr(int row, int slot) {
+    return row * kVStride + 8 * ((slot >> 3) ^ ((row >> 3) & 7)) + (slot & 7);
 }
 
 // Reductions across the 4 lane groups of a token column (lanes l, l^16,
@@ -82,18 +94,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int lane = t & 63, wave = t >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const uint32_t g = blockIdx.y;
-    const uint32_t tile = a.n_tiles - 1 - blockIdx.x;        // heaviest first
-    const uint32_t tile0 = tile * kTileTok;
-    const uint32_t wtok0 = tile0 + 16 * (wave & 3);           // first token of this wave
-    const uint32_t h0 = g * kGroup + kHeadsPerWave * (wave >> 2);   // first query head of this wave
-    const uint32_t my_tok = wtok0 + lr;                       // token of this lane's column
-    const uint32_t last_tok = min(tile0 + kTileTok, a.m_tokens) - 1;
-    const uint32_t kend = a.causal ? a.pos + last_tok + 1 : a.pos;   // rows the tile needs
+    const uint32_t tile_a = blockIdx.x, tile_b = a.n_tiles - 1 - blockIdx.x;   // tile_b >= tile_a
+    const uint32_t tile = (wave & 4) ? tile_b : tile_a;
+    const bool wave_live = !((wave & 4) && tile_b == tile_a) &&
+                           tile * kPrefillTileTok + 16 * (wave & 1) < a.m_tokens;
+    const uint32_t wtok0 = tile * kPrefillTileTok + 16 * (wave & 1);   // first token of this wave
+    const uint32_t h0 = g * kGroup + kHeadsPerWave * ((wave >> 1) & 1); // first query head
+    const uint32_t my_tok = wtok0 + lr;                                   // this lane's column
+    const uint32_t last_b = min(tile_b * kPrefillTileTok + kPrefillTileTok, a.m_tokens) - 1;
+    const uint32_t kend = a.causal ? a.pos + last_b + 1 : a.pos;         // rows the pair needs
     const uint32_t n_chunks = (kend + kChunk - 1) / kChunk;
     // Rows this wave's tokens can see: [0, wave_kend).
     const uint32_t wave_last = min(wtok0 + 15, a.m_tokens - 1);
     const uint32_t wave_kend = a.causal ? a.pos + wave_last + 1 : a.pos;
-    const bool wave_live = wtok0 < a.m_tokens;
     const uint32_t my_kend = a.causal ? a.pos + my_tok + 1 : a.pos;
 
     // ---- Q^T fragments (B operand of S^T = K Q^T), 2 heads x 4 k-steps ----
@@ -103,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             U4 raw = {{0, 0, 0, 0}};
-            if (my_tok < a.m_tokens) {
+            if (wave_live && my_tok < a.m_tokens) {
                 raw = *reinterpret_cast<const U4*>(a.q + static_cast<uint64_t>(my_tok) * a.q_stride +
                                                    (h0 + h) * kHeadDim + 32 * kk + 8 * lg);
             }
@@ -122,47 +135,51 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const float c2 = a.scale * 1.4426950408889634f;   // scores in log2 units
 
     // ---- staging ------------------------------------------------------------
-    // Threads 0..255 stage K: thread owns chunk row (t >> 3), dims
-    //   [16 (t & 7), +16) -> row-major LDS writes of 2 x 16 bytes.
-    // Threads 256..511 stage V: thread owns chunk row (t & 31), dims
-    //   [16 ((t >> 5) & 7), +16) -> 16 transposed 2-byte writes into one V^T
-    //   column; the 32 rows of a wave fill 32 consecutive columns.
+    // K: thread owns chunk row (t >> 3), dims [16 (t & 7), +16).
+    // V: thread owns chunk rows 2u, 2u+1 (u = t >> 4), dims [8 (t & 15), +8);
+    //    it writes each dim's two values as one 4-byte word of V^T (the rows
+    //    of a key pair are adjacent slots).
     // Loads are unconditional from a clamped row (a predicated load becomes a
     // branch that drains all outstanding loads); rows past kend are zeroed
-    // through their scale. Two register stages give a prefetch distance of 2
-    // chunks: chunk c+2 is loaded while chunk c is computed and c+1 is staged.
-    const bool stage_k = t < 256;
-    const int srow = stage_k ? (t >> 3) : (t & 31);
-    const int sseg = stage_k ? (t & 7) : ((t >> 5) & 7);
-    const int8_t* sqs = stage_k ? a.k.qs : a.v.qs;
-    const float* sd = stage_k ? a.k.d : a.v.d;
+    // through their scale.
+    const int krow = t >> 3, kseg = t & 7;
+    const int vu = t >> 4, vdq = t & 15;
     const uint64_t kv_dim = a.kv_dim;
     const uint32_t nb_row = a.kv_dim / kBlock;
-    const uint32_t scol = g * kHeadDim + 16 * sseg, sdcol = g * (kHeadDim / kBlock) + (sseg >> 1);
-    struct Stage { U4 q; float d; };
+    const uint32_t kcol = g * kHeadDim + 16 * kseg, kdcol = g * (kHeadDim / kBlock) + (kseg >> 1);
+    const uint32_t vcol = g * kHeadDim + 8 * vdq, vdcol = g * (kHeadDim / kBlock) + (vdq >> 2);
+    struct Stage { U4 kq; uint2 v0, v1; float kd, vd0, vd1; };
     auto load_chunk = [&](Stage& S, uint32_t c) {
-        const uint32_t r = c * kChunk + srow;
-        const uint64_t rc = min(r, kend - 1);
-        S.q = *reinterpret_cast<const U4*>(sqs + rc * kv_dim + scol);
-        S.d = sd[rc * nb_row + sdcol];
-        if (r >= kend) S.d = 0.0f;
+        const uint32_t kr = c * kChunk + krow, vr = c * kChunk + 2 * vu;
+        const uint64_t krc = min(kr, kend - 1), vr0 = min(vr, kend - 1), vr1 = min(vr + 1, kend - 1);
+        S.kq = *reinterpret_cast<const U4*>(a.k.qs + krc * kv_dim + kcol);
+        S.v0 = *reinterpret_cast<const uint2*>(a.v.qs + vr0 * kv_dim + vcol);
+        S.v1 = *reinterpret_cast<const uint2*>(a.v.qs + vr1 * kv_dim + vcol);
+        S.kd = a.k.d[krc * nb_row + kdcol];
+        S.vd0 = a.v.d[vr0 * nb_row + vdcol];
+        S.vd1 = a.v.d[vr1 * nb_row + vdcol];
+        if (kr >= kend) S.kd = 0.0f;
+        if (vr >= kend) S.vd0 = 0.0f;
+        if (vr + 1 >= kend) S.vd1 = 0.0f;
     };
     auto store_chunk = [&](const Stage& S, int buf) {
-        if (stage_k) {
-            U4 lo, hi;
+        U4 lo, hi;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                lo.w[i] = pack2(S.d * i8f(S.q.w[i >> 1], 2 * (i & 1)), S.d * i8f(S.q.w[i >> 1], 2 * (i & 1) + 1));
-                hi.w[i] = pack2(S.d * i8f(S.q.w[2 + (i >> 1)], 2 * (i & 1)),
-                                S.d * i8f(S.q.w[2 + (i >> 1)], 2 * (i & 1) + 1));
-            }
-            uint16_t* kr = &k_lds[buf][srow * kKStride + 16 * sseg];
-            *reinterpret_cast<U4*>(kr) = lo;
-            *reinterpret_cast<U4*>(kr + 8) = hi;
-        } else {
-            uint16_t* vc = &v_lds[buf][(16 * sseg) * kVStride + v_slot(srow)];
+        for (int i = 0; i < 4; i++) {
+            lo.w[i] = pack2(S.kd * i8f(S.kq.w[i >> 1], 2 * (i & 1)), S.kd * i8f(S.kq.w[i >> 1], 2 * (i & 1) + 1));
+            hi.w[i] = pack2(S.kd * i8f(S.kq.w[2 + (i >> 1)], 2 * (i & 1)),
+                            S.kd * i8f(S.kq.w[2 + (i >> 1)], 2 * (i & 1) + 1));
+        }
+        uint16_t* kr = &k_lds[buf][krow * kKStride + 16 * kseg];
+        *reinterpret_cast<U4*>(kr) = lo;
+        *reinterpret_cast<U4*>(kr + 8) = hi;
+        const int slot = v_slot(2 * vu);   // even; 2u + 1 sits in slot + 1
+        const uint32_t w0[2] = {S.v0.x, S.v0.y}, w1[2] = {S.v1.x, S.v1.y};
 #pragma unroll
-            for (int i = 0; i < 16; i++) vc[i * kVStride] = f2h(S.d * i8f(S.q.w[i >> 2], i & 3));
+        for (int i = 0; i < 8; i++) {
+            const int row = 8 * vdq + i;
+            *reinterpret_cast<uint32_t*>(&v_lds[buf][v_addr(row, slot)]) =
+                pack2(S.vd0 * i8f(w0[i >> 2], i & 3), S.vd1 * i8f(w1[i >> 2], i & 3));
         }
     };
 
@@ -181,10 +198,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
         if (wave_live && key0 < wave_kend) {
             const uint16_t* kb = k_lds[buf];
             const uint16_t* vb = v_lds[buf];
-            // ---- S^T = K Q^T: 2 key sub-tiles x 2 heads --------------------
-            f32x4 s[kHeadsPerWave][2];
+            // ---- S^T = K Q^T: 4 key sub-tiles x 2 heads --------------------
+            f32x4 s[kHeadsPerWave][kSub];
 #pragma unroll
-            for (int st2 = 0; st2 < 2; st2++) {
+            for (int st2 = 0; st2 < kSub; st2++) {
                 f16x8 ka[4];
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++)
@@ -202,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++)
 #pragma unroll
-                for (int st2 = 0; st2 < 2; st2++)
+                for (int st2 = 0; st2 < kSub; st2++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         float v = s[h][st2][j] * c2;
@@ -210,11 +227,13 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
                         s[h][st2][j] = v;
                     }
             // ---- online softmax + P^T fragments ------------------------------
-            f16x8 pb[kHeadsPerWave];
+            f16x8 pb[kHeadsPerWave][kSub / 2];
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++) {
-                float cm = fmaxf(fmaxf(fmaxf(s[h][0][0], s[h][0][1]), fmaxf(s[h][0][2], s[h][0][3])),
-                                 fmaxf(fmaxf(s[h][1][0], s[h][1][1]), fmaxf(s[h][1][2], s[h][1][3])));
+                float cm = -INFINITY;
+#pragma unroll
+                for (int st2 = 0; st2 < kSub; st2++)
+                    cm = fmaxf(cm, fmaxf(fmaxf(s[h][st2][0], s[h][st2][1]), fmaxf(s[h][st2][2], s[h][st2][3])));
                 cm = group_max(cm);
                 // Lazy rescale: the running max of a row moves only when the chunk
                 // max exceeds it by more than kLazy; p then stays below 2^kLazy,
@@ -228,27 +247,34 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                     for (int dt = 0; dt < 8; dt++) o[h][dt] *= alpha;
                 }
-                float p[8];
                 float ps = 0.0f;
 #pragma unroll
-                for (int st2 = 0; st2 < 2; st2++)
+                for (int kc = 0; kc < kSub / 2; kc++) {
+                    float p[8];
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        p[4 * st2 + j] = __builtin_amdgcn_exp2f(s[h][st2][j] - m_run[h]);
-                        ps += p[4 * st2 + j];
-                    }
+                    for (int half = 0; half < 2; half++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            p[4 * half + j] = __builtin_amdgcn_exp2f(s[h][2 * kc + half][j] - m_run[h]);
+                            ps += p[4 * half + j];
+                        }
+                    U4 pk;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) pk.w[i] = pack2(p[2 * i], p[2 * i + 1]);
+                    pb[h][kc] = __builtin_bit_cast(f16x8, pk);
+                }
                 l_run[h] += ps;
-                U4 pk;
-#pragma unroll
-                for (int i = 0; i < 4; i++) pk.w[i] = pack2(p[2 * i], p[2 * i + 1]);
-                pb[h] = __builtin_bit_cast(f16x8, pk);
             }
             // ---- O^T += V^T P^T ------------------------------------------------
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
-                const f16x8 va = *reinterpret_cast<const f16x8*>(vb + (16 * dt + lr) * kVStride + 8 * lg);
+                const int row = 16 * dt + lr;
 #pragma unroll
-                for (int h = 0; h < kHeadsPerWave; h++) o[h][dt] = mfma16(va, pb[h], o[h][dt]);
+                for (int kc = 0; kc < kSub / 2; kc++) {
+                    const f16x8 va = *reinterpret_cast<const f16x8*>(vb + v_addr(row, 32 * kc + 8 * lg));
+#pragma unroll
+                    for (int h = 0; h < kHeadsPerWave; h++) o[h][dt] = mfma16(va, pb[h][kc], o[h][dt]);
+                }
             }
         }
         if (c + 1 < n_chunks) store_chunk(st, buf ^ 1);
@@ -278,7 +304,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(prefill_kernel, dim3(a.n_tiles, n_kv_head), dim3(kThreads), 0, s, a);
+    const uint32_t n_pairs = (a.n_tiles + 1) / 2;
+    hipLaunchKernelGGL(prefill_kernel, dim3(n_pairs, n_kv_head), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

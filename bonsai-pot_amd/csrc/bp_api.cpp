@@ -451,7 +451,7 @@ bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t
     a.m_tokens = m_tokens;
     a.pos = pos;
     a.causal = is_prefill ? 1u : 0u;
-    a.n_tiles = (m_tokens + 63) / 64;
+    a.n_tiles = (m_tokens + bp::kPrefillTileTok - 1) / bp::kPrefillTileTok;
     a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:524
     return hip_check(m, bp::launch_prefill(a, m->cfg.n_kv_head, m->stream), "attention launch");
 }

@@ -11,6 +11,7 @@ namespace bp {
 constexpr uint32_t kHeadDim = 128;   // Bonsai head_dim (src/model.rs:1179-1183)
 constexpr uint32_t kGroup = 4;       // Q heads per KV head (attention_split.wgsl:150)
 constexpr uint32_t kBlock = 32;      // Q8_0 block (src/forward.rs:40-47)
+constexpr uint32_t kPrefillTileTok = 32;   // query tokens per prefill tile
 
 // One (layer, kind) view of a Q8_0 KV buffer: FP32 scales at d (index
 // (row*kv_dim + e)/32), int8 quants at qs (index row*kv_dim + e).
@@ -78,7 +79,7 @@ struct PrefillArgs {
     uint32_t m_tokens;
     uint32_t pos;             // first query's RoPE/cache position when causal
     uint32_t causal;          // 1: token m sees rows [0, pos+m]; 0: rows [0, pos)
-    uint32_t n_tiles;         // ceil(m_tokens / 64)
+    uint32_t n_tiles;         // ceil(m_tokens / kPrefillTileTok)
     float scale;
 };
 

@@ -4,28 +4,33 @@
 // attends rows [0, cur) with cur = causal ? pos + m + 1 : pos, f32 softmax,
 // f16 output — computed as a flash-attention over LDS tiles:
 //
-//  * Query tokens form tiles of 32. A 512-thread workgroup owns one KV head
-//    and a zig-zag PAIR of tiles (p, n_tiles-1-p): waves 0-3 take tile p,
-//    waves 4-7 tile n_tiles-1-p, each wave 16 tokens x 2 GQA heads. Under the
-//    causal mask the two tiles' work sums to the same amount for every pair,
-//    so the 256 CUs finish together, and each SIMD holds one wave of each tile
-//    (one's softmax overlaps the other's MFMAs). Both tiles read the same cache
-//    rows (the light tile's range is a prefix of the heavy one's), so every
-//    chunk is staged once.
-//  * K/V are consumed in chunks of 64 rows. Every thread stages 16 bytes of K
-//    and 2 x 8 bytes of V per chunk (register prefetch distance of two
-//    chunks), dequantizing Q8_0 to f16 (d * q, one rounding) into
-//    double-buffered LDS: K row-major, V transposed (dim-major, 16-byte groups
-//    XOR-swizzled by row to spread the transposed writes over the banks), so
-//    both MFMA operands are single 16-byte LDS reads.
+//  * Query tokens form tiles of 32; a "unit" is 16 tokens x 2 GQA heads (one
+//    wave's MFMA columns). A 512-thread workgroup owns one KV head and a
+//    zig-zag PAIR of tiles: light tile A = blockIdx.x, heavy tile
+//    B = n_tiles-1-blockIdx.x. Wave w (SIMD w & 3) owns unit (w & 3) of tile
+//    A if w < 4, of tile B otherwise, so each SIMD holds one A wave and one B
+//    wave (one's softmax overlaps the other's MFMAs).
+//  * Work balance (split-K inside the workgroup): with n_A / n_B the 64-row
+//    chunks tiles A / B attend and mid = ceil((n_A + n_B) / 2), the B waves
+//    take B's chunks [0, mid) while the A waves take A's chunks [0, n_A) and
+//    then B's chunks [mid, n_B); the two halves of B are merged through LDS at
+//    the end (log-sum-exp). Every pair then runs ~(n_A + n_B) / 2 iterations
+//    with two busy waves per SIMD, so the 256 CUs finish together. (A middle
+//    tile paired with itself is simply split between its two waves.)
+//  * Chunks are staged from two streams — stream 1 serves chunk i (A waves
+//    while i < n_A, B waves), stream 2 serves B's chunk mid + i - n_A — each
+//    dequantized from Q8_0 to f16 (d * q, one rounding) into double-buffered
+//    LDS: K row-major, V transposed (dim-major, 16-byte groups XOR-swizzled by
+//    row against bank conflicts), so both MFMA operands are single 16-byte
+//    LDS reads. Loads for iteration i+1 are in flight while i is computed.
 //  * S^T = K Q^T with v_mfma_f32_16x16x32_f16 (K = 32 dims per step): the
 //    output fragment of lane l holds 8 keys of token (l % 16) per 32 keys. With
 //    the keys stored in V^T in the matching permuted order, those fragments are
 //    directly the B operand of O^T = V^T P^T — no shuffles, no LDS trip.
-//  * Online softmax in the exp2 domain (scale * log2 e folded into one
-//    multiply), row max across the 4 lane groups by swizzle/permute, and a
-//    lazy running max (moved only by more than kLazy log2 units), so the O
-//    accumulators are almost never touched by VALU.
+//  * Online softmax in the exp2 domain (p = exp2(s * scale * log2 e - m) is
+//    one FMA and one exp), row max across the 4 lane groups by
+//    swizzle/permute, and a lazy running max (moved only by more than kLazy
+//    log2 units), so the O accumulators are almost never touched by VALU.
 //
 // MFMA fragment layout used (v_mfma_f32_16x16x32_f16, lane l, g = l / 16):
 //   A[i][k]: lane holds A[l % 16][8g .. 8g+7]
@@ -46,6 +51,9 @@ constexpr int kChunk = 64;               // cache rows per LDS chunk
 constexpr int kSub = kChunk / 16;        // 16-row S^T sub-tiles per chunk
 constexpr int kKStride = kHeadDim + 8;   // halves per K row in LDS (pad vs bank conflicts)
 constexpr int kVStride = kChunk + 8;     // halves per V^T row in LDS
+constexpr int kKHalves = kChunk * kKStride;
+constexpr int kVHalves = kHeadDim * kVStride;
+constexpr int kBufHalves = kKHalves + kVHalves;   // one staged chunk
 constexpr float kLazy = 8.0f;            // lazy-rescale threshold (log2 units)
 
 struct alignas(16) U4 { uint32_t w[4]; };
@@ -87,52 +95,79 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kChunk * kKStride];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kHeadDim * kVStride];
+    // lds[stream][buf]: staged chunk (K rows then V^T rows), 2 streams x 2 buffers.
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int lr = lane & 15, lg = lane >> 4;
+    const bool is_b = (wave & 4) != 0;               // B wave (heavy tile) or A wave
     const uint32_t g = blockIdx.y;
     const uint32_t tile_a = blockIdx.x, tile_b = a.n_tiles - 1 - blockIdx.x;   // tile_b >= tile_a
-    const uint32_t tile = (wave & 4) ? tile_b : tile_a;
-    const bool wave_live = !((wave & 4) && tile_b == tile_a) &&
-                           tile * kPrefillTileTok + 16 * (wave & 1) < a.m_tokens;
-    const uint32_t wtok0 = tile * kPrefillTileTok + 16 * (wave & 1);   // first token of this wave
-    const uint32_t h0 = g * kGroup + kHeadsPerWave * ((wave >> 1) & 1); // first query head
-    const uint32_t my_tok = wtok0 + lr;                                   // this lane's column
-    const uint32_t last_b = min(tile_b * kPrefillTileTok + kPrefillTileTok, a.m_tokens) - 1;
-    const uint32_t kend = a.causal ? a.pos + last_b + 1 : a.pos;         // rows the pair needs
-    const uint32_t n_chunks = (kend + kChunk - 1) / kChunk;
-    // Rows this wave's tokens can see: [0, wave_kend).
-    const uint32_t wave_last = min(wtok0 + 15, a.m_tokens - 1);
-    const uint32_t wave_kend = a.causal ? a.pos + wave_last + 1 : a.pos;
-    const uint32_t my_kend = a.causal ? a.pos + my_tok + 1 : a.pos;
-
-    // ---- Q^T fragments (B operand of S^T = K Q^T), 2 heads x 4 k-steps ----
-    f16x8 qb[kHeadsPerWave][4];
-#pragma unroll
-    for (int h = 0; h < kHeadsPerWave; h++) {
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            U4 raw = {{0, 0, 0, 0}};
-            if (wave_live && my_tok < a.m_tokens) {
-                raw = *reinterpret_cast<const U4*>(a.q + static_cast<uint64_t>(my_tok) * a.q_stride +
-                                                   (h0 + h) * kHeadDim + 32 * kk + 8 * lg);
-            }
-            qb[h][kk] = __builtin_bit_cast(f16x8, raw);
-        }
-    }
-
-    f32x4 o[kHeadsPerWave][8];
-#pragma unroll
-    for (int h = 0; h < kHeadsPerWave; h++)
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[kHeadsPerWave], l_run[kHeadsPerWave];
-#pragma unroll
-    for (int h = 0; h < kHeadsPerWave; h++) { m_run[h] = -INFINITY; l_run[h] = 0.0f; }
+    const uint32_t h0 = g * kGroup + kHeadsPerWave * ((wave >> 1) & 1);        // first query head
+    const uint32_t utok = 16 * (wave & 1);            // unit's first token within its tile
     const float c2 = a.scale * 1.4426950408889634f;   // scores in log2 units
+
+    // Rows [0, kend) that tile x attends, and its chunk count.
+    auto tile_kend = [&](uint32_t tile) {
+        const uint32_t last = min(tile * kPrefillTileTok + kPrefillTileTok, a.m_tokens) - 1;
+        return a.causal ? a.pos + last + 1 : a.pos;
+    };
+    const uint32_t kend_b = tile_kend(tile_b);
+    const uint32_t n_b = (kend_b + kChunk - 1) / kChunk;
+    const uint32_t n_a = tile_b == tile_a ? 0u : (tile_kend(tile_a) + kChunk - 1) / kChunk;
+    const uint32_t mid = (n_a + n_b + 1) / 2;        // B waves: [0, mid); A waves: [mid, n_b) of B
+    const uint32_t n_iter = mid;                     // >= n_a + (n_b - mid)
+
+    // ---- per-wave unit state -------------------------------------------------
+    uint32_t wtok0 = 0, my_tok = 0, my_kend = 0, wave_kend = 0;
+    bool unit_live = false;
+    f16x8 qb[kHeadsPerWave][4];
+    f32x4 o[kHeadsPerWave][8];
+    float m_run[kHeadsPerWave], l_run[kHeadsPerWave];
+    auto start_unit = [&](uint32_t tile) {
+        wtok0 = tile * kPrefillTileTok + utok;
+        my_tok = wtok0 + lr;
+        unit_live = wtok0 < a.m_tokens;
+        const uint32_t wave_last = min(wtok0 + 15, a.m_tokens - 1);
+        wave_kend = unit_live ? (a.causal ? a.pos + wave_last + 1 : a.pos) : 0u;
+        my_kend = a.causal ? a.pos + my_tok + 1 : a.pos;
+#pragma unroll
+        for (int h = 0; h < kHeadsPerWave; h++) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                U4 raw = {{0, 0, 0, 0}};
+                if (unit_live && my_tok < a.m_tokens)
+                    raw = *reinterpret_cast<const U4*>(a.q + static_cast<uint64_t>(my_tok) * a.q_stride +
+                                                       (h0 + h) * kHeadDim + 32 * kk + 8 * lg);
+                qb[h][kk] = __builtin_bit_cast(f16x8, raw);
+            }
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            m_run[h] = -INFINITY;
+            l_run[h] = 0.0f;
+        }
+    };
+    // Normalize and store O (lane: token my_tok, dims 16dt + 4lg + j); l_run
+    // must already be summed over the token's 4 lane groups.
+    auto write_unit = [&]() {
+        if (!unit_live || my_tok >= a.m_tokens) return;
+#pragma unroll
+        for (int h = 0; h < kHeadsPerWave; h++) {
+            const float inv_l = 1.0f / l_run[h];
+            uint16_t* out = a.out + static_cast<uint64_t>(my_tok) * a.q_stride + (h0 + h) * kHeadDim;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                uint2 w;
+                w.x = pack2(o[h][dt][0] * inv_l, o[h][dt][1] * inv_l);
+                w.y = pack2(o[h][dt][2] * inv_l, o[h][dt][3] * inv_l);
+                *reinterpret_cast<uint2*>(out + 16 * dt + 4 * lg) = w;
+            }
+        }
+    };
+    // A waves start on tile A (or, for a self-paired middle tile, directly on
+    // the second half of it); B waves on tile B.
+    start_unit(is_b || n_a == 0 ? tile_b : tile_a);
 
     // ---- staging ------------------------------------------------------------
     // K: thread owns chunk row (t >> 3), dims [16 (t & 7), +16).
@@ -140,7 +175,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     //    it writes each dim's two values as one 4-byte word of V^T (the rows
     //    of a key pair are adjacent slots).
     // Loads are unconditional from a clamped row (a predicated load becomes a
-    // branch that drains all outstanding loads); rows past kend are zeroed
+    // branch that drains all outstanding loads); rows past kend_b are zeroed
     // through their scale.
     const int krow = t >> 3, kseg = t & 7;
     const int vu = t >> 4, vdq = t & 15;
@@ -151,18 +186,18 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     struct Stage { U4 kq; uint2 v0, v1; float kd, vd0, vd1; };
     auto load_chunk = [&](Stage& S, uint32_t c) {
         const uint32_t kr = c * kChunk + krow, vr = c * kChunk + 2 * vu;
-        const uint64_t krc = min(kr, kend - 1), vr0 = min(vr, kend - 1), vr1 = min(vr + 1, kend - 1);
+        const uint64_t krc = min(kr, kend_b - 1), vr0 = min(vr, kend_b - 1), vr1 = min(vr + 1, kend_b - 1);
         S.kq = *reinterpret_cast<const U4*>(a.k.qs + krc * kv_dim + kcol);
         S.v0 = *reinterpret_cast<const uint2*>(a.v.qs + vr0 * kv_dim + vcol);
         S.v1 = *reinterpret_cast<const uint2*>(a.v.qs + vr1 * kv_dim + vcol);
         S.kd = a.k.d[krc * nb_row + kdcol];
         S.vd0 = a.v.d[vr0 * nb_row + vdcol];
         S.vd1 = a.v.d[vr1 * nb_row + vdcol];
-        if (kr >= kend) S.kd = 0.0f;
-        if (vr >= kend) S.vd0 = 0.0f;
-        if (vr + 1 >= kend) S.vd1 = 0.0f;
+        if (kr >= kend_b) S.kd = 0.0f;
+        if (vr >= kend_b) S.vd0 = 0.0f;
+        if (vr + 1 >= kend_b) S.vd1 = 0.0f;
     };
-    auto store_chunk = [&](const Stage& S, int buf) {
+    auto store_chunk = [&](const Stage& S, uint16_t* buf) {
         U4 lo, hi;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -170,135 +205,175 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             hi.w[i] = pack2(S.kd * i8f(S.kq.w[2 + (i >> 1)], 2 * (i & 1)),
                             S.kd * i8f(S.kq.w[2 + (i >> 1)], 2 * (i & 1) + 1));
         }
-        uint16_t* kr = &k_lds[buf][krow * kKStride + 16 * kseg];
+        uint16_t* kr = buf + krow * kKStride + 16 * kseg;
         *reinterpret_cast<U4*>(kr) = lo;
         *reinterpret_cast<U4*>(kr + 8) = hi;
+        uint16_t* vb = buf + kKHalves;
         const int slot = v_slot(2 * vu);   // even; 2u + 1 sits in slot + 1
         const uint32_t w0[2] = {S.v0.x, S.v0.y}, w1[2] = {S.v1.x, S.v1.y};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int row = 8 * vdq + i;
-            *reinterpret_cast<uint32_t*>(&v_lds[buf][v_addr(row, slot)]) =
+            *reinterpret_cast<uint32_t*>(vb + v_addr(row, slot)) =
                 pack2(S.vd0 * i8f(w0[i >> 2], i & 3), S.vd1 * i8f(w1[i >> 2], i & 3));
         }
     };
 
-    Stage S0, S1;
-    load_chunk(S0, 0);
-    if (n_chunks > 1) load_chunk(S1, 1);
-    store_chunk(S0, 0);
-    __syncthreads();
-
-    // One chunk: prefetch chunk c+2 into `ld` (free: its chunk c was staged
-    // last iteration), compute chunk c from LDS, stage chunk c+1 from `st`.
-    auto step = [&](Stage& ld, const Stage& st, uint32_t c) {
-        const int buf = c & 1;
-        if (c + 2 < n_chunks) load_chunk(ld, c + 2);
-        const uint32_t key0 = c * kChunk;
-        if (wave_live && key0 < wave_kend) {
-            const uint16_t* kb = k_lds[buf];
-            const uint16_t* vb = v_lds[buf];
-            // ---- S^T = K Q^T: 4 key sub-tiles x 2 heads --------------------
-            f32x4 s[kHeadsPerWave][kSub];
+    // ---- one chunk of attention for the current unit --------------------------
+    auto compute = [&](const uint16_t* buf, uint32_t key0) {
+        if (!unit_live || key0 >= wave_kend) return;
+        const uint16_t* kb = buf;
+        const uint16_t* vb = buf + kKHalves;
+        // S^T = K Q^T, k-step outer: each step issues 8 independent MFMAs.
+        f32x4 s[kHeadsPerWave][kSub];
 #pragma unroll
-            for (int st2 = 0; st2 < kSub; st2++) {
-                f16x8 ka[4];
+        for (int h = 0; h < kHeadsPerWave; h++)
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++)
-                    ka[kk] = *reinterpret_cast<const f16x8*>(kb + (16 * st2 + lr) * kKStride + 32 * kk + 8 * lg);
+            for (int st2 = 0; st2 < kSub; st2++) s[h][st2] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int h = 0; h < kHeadsPerWave; h++) {
-                    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < 4; kk++) {
+            f16x8 ka[kSub];
 #pragma unroll
-                    for (int kk = 0; kk < 4; kk++) acc = mfma16(ka[kk], qb[h][kk], acc);
-                    s[h][st2] = acc;
-                }
-            }
-            // ---- mask (only chunks that reach past the earliest visible row)
-            const bool need_mask = key0 + kChunk > (a.causal ? a.pos + wtok0 + 1 : a.pos);
+            for (int st2 = 0; st2 < kSub; st2++)
+                ka[st2] = *reinterpret_cast<const f16x8*>(kb + (16 * st2 + lr) * kKStride + 32 * kk + 8 * lg);
+#pragma unroll
+            for (int st2 = 0; st2 < kSub; st2++)
+#pragma unroll
+                for (int h = 0; h < kHeadsPerWave; h++) s[h][st2] = mfma16(ka[st2], qb[h][kk], s[h][st2]);
+        }
+        // Mask (only chunks that reach past the unit's earliest visible row);
+        // raw scores, the scale is applied inside the exponent.
+        const bool need_mask = key0 + kChunk > (a.causal ? a.pos + wtok0 + 1 : a.pos);
+        if (need_mask) {
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++)
 #pragma unroll
                 for (int st2 = 0; st2 < kSub; st2++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        float v = s[h][st2][j] * c2;
-                        if (need_mask && key0 + 16 * st2 + 4 * lg + j >= my_kend) v = -INFINITY;
-                        s[h][st2][j] = v;
-                    }
-            // ---- online softmax + P^T fragments ------------------------------
-            f16x8 pb[kHeadsPerWave][kSub / 2];
+                    for (int j = 0; j < 4; j++)
+                        if (key0 + 16 * st2 + 4 * lg + j >= my_kend) s[h][st2][j] = -INFINITY;
+        }
+        // Online softmax (m_run in log2 units) + P^T fragments.
+        f16x8 pb[kHeadsPerWave][kSub / 2];
 #pragma unroll
-            for (int h = 0; h < kHeadsPerWave; h++) {
-                float cm = -INFINITY;
+        for (int h = 0; h < kHeadsPerWave; h++) {
+            float cm = -INFINITY;
 #pragma unroll
-                for (int st2 = 0; st2 < kSub; st2++)
-                    cm = fmaxf(cm, fmaxf(fmaxf(s[h][st2][0], s[h][st2][1]), fmaxf(s[h][st2][2], s[h][st2][3])));
-                cm = group_max(cm);
-                // Lazy rescale: the running max of a row moves only when the chunk
-                // max exceeds it by more than kLazy; p then stays below 2^kLazy,
-                // which f16 P and the f32 accumulators hold as well as p <= 1.
-                const bool up = cm > m_run[h] + kLazy;
-                if (__any(up)) {
-                    const float m_new = up ? cm : m_run[h];
-                    const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 from -inf
-                    m_run[h] = m_new;
-                    l_run[h] *= alpha;
+            for (int st2 = 0; st2 < kSub; st2++)
+                cm = fmaxf(cm, fmaxf(fmaxf(s[h][st2][0], s[h][st2][1]), fmaxf(s[h][st2][2], s[h][st2][3])));
+            cm = group_max(cm) * c2;
+            // Lazy rescale: the running max of a row moves only when the chunk
+            // max exceeds it by more than kLazy; p then stays below 2^kLazy,
+            // which f16 P and the f32 accumulators hold as well as p <= 1.
+            const bool up = cm > m_run[h] + kLazy;
+            if (__any(up)) {
+                const float m_new = up ? cm : m_run[h];
+                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 from -inf
+                m_run[h] = m_new;
+                l_run[h] *= alpha;
 #pragma unroll
-                    for (int dt = 0; dt < 8; dt++) o[h][dt] *= alpha;
-                }
-                float ps = 0.0f;
-#pragma unroll
-                for (int kc = 0; kc < kSub / 2; kc++) {
-                    float p[8];
-#pragma unroll
-                    for (int half = 0; half < 2; half++)
-#pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            p[4 * half + j] = __builtin_amdgcn_exp2f(s[h][2 * kc + half][j] - m_run[h]);
-                            ps += p[4 * half + j];
-                        }
-                    U4 pk;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) pk.w[i] = pack2(p[2 * i], p[2 * i + 1]);
-                    pb[h][kc] = __builtin_bit_cast(f16x8, pk);
-                }
-                l_run[h] += ps;
+                for (int dt = 0; dt < 8; dt++) o[h][dt] *= alpha;
             }
-            // ---- O^T += V^T P^T ------------------------------------------------
+            const float neg_m = -m_run[h];
+            float ps = 0.0f;
+#pragma unroll
+            for (int kc = 0; kc < kSub / 2; kc++) {
+                float p[8];
+#pragma unroll
+                for (int half = 0; half < 2; half++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        p[4 * half + j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][2 * kc + half][j], c2, neg_m));
+                        ps += p[4 * half + j];
+                    }
+                U4 pk;
+#pragma unroll
+                for (int i = 0; i < 4; i++) pk.w[i] = pack2(p[2 * i], p[2 * i + 1]);
+                pb[h][kc] = __builtin_bit_cast(f16x8, pk);
+            }
+            l_run[h] += ps;
+        }
+        // O^T += V^T P^T: per k-step 16 independent MFMAs.
+#pragma unroll
+        for (int kc = 0; kc < kSub / 2; kc++) {
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
-                const int row = 16 * dt + lr;
+                const f16x8 va = *reinterpret_cast<const f16x8*>(vb + v_addr(16 * dt + lr, 32 * kc + 8 * lg));
 #pragma unroll
-                for (int kc = 0; kc < kSub / 2; kc++) {
-                    const f16x8 va = *reinterpret_cast<const f16x8*>(vb + v_addr(row, 32 * kc + 8 * lg));
-#pragma unroll
-                    for (int h = 0; h < kHeadsPerWave; h++) o[h][dt] = mfma16(va, pb[h][kc], o[h][dt]);
-                }
+                for (int h = 0; h < kHeadsPerWave; h++) o[h][dt] = mfma16(va, pb[h][kc], o[h][dt]);
             }
         }
-        if (c + 1 < n_chunks) store_chunk(st, buf ^ 1);
-        __syncthreads();
     };
-    for (uint32_t c = 0; c < n_chunks; c += 2) {
-        step(S0, S1, c);
-        if (c + 1 < n_chunks) step(S1, S0, c + 1);
+
+    // ---- main loop: iteration i computes stream-1 chunk i and (i >= n_a)
+    // stream-2 chunk mid + i - n_a; loads for i+1 are issued first -----------
+    auto c1_of = [&](uint32_t i) { return i; };                      // valid while i < mid
+    auto has2 = [&](uint32_t i) { return i >= n_a && mid + (i - n_a) < n_b; };
+    auto c2_of = [&](uint32_t i) { return mid + (i - n_a); };
+    Stage s1, s2;
+    load_chunk(s1, c1_of(0));
+    if (has2(0)) load_chunk(s2, c2_of(0));
+    store_chunk(s1, lds[0][0]);
+    if (has2(0)) store_chunk(s2, lds[1][0]);
+    __syncthreads();
+    for (uint32_t i = 0; i < n_iter; i++) {
+        const int buf = i & 1;
+        const bool next = i + 1 < n_iter, next2 = next && has2(i + 1);
+        if (next) load_chunk(s1, c1_of(i + 1));
+        if (next2) load_chunk(s2, c2_of(i + 1));
+        // One call site: a wave computes stream 1 (B waves; A waves while on
+        // tile A) or stream 2 (A waves once on B's second half).
+        const bool on1 = is_b || i < n_a;
+        if (on1 || has2(i)) compute(lds[on1 ? 0 : 1][buf], (on1 ? c1_of(i) : c2_of(i)) * kChunk);
+        if (!is_b && i + 1 == n_a) {   // tile A done: store it, move to B's second half
+#pragma unroll
+            for (int h = 0; h < kHeadsPerWave; h++) l_run[h] = group_sum(l_run[h]);
+            write_unit();
+            start_unit(tile_b);
+        }
+        if (next) store_chunk(s1, lds[0][buf ^ 1]);
+        if (next2) store_chunk(s2, lds[1][buf ^ 1]);
+        __syncthreads();
     }
 
-    if (!wave_live || my_tok >= a.m_tokens) return;
-    // ---- normalize and write O (lane: token my_tok, dims 16dt + 4lg + j) ----
+    // ---- merge the two halves of tile B: A waves hand (O, m, l) to B waves --
+    // (the staging buffers are free: every wave is past the last barrier).
+    float* xo = reinterpret_cast<float*>(&lds[0][0][0]);   // [4 units][2 h][8 dt][4][64 lanes]
+    float* xml = xo + 4 * kHeadsPerWave * 8 * 4 * 64;      // [4 units][2 h][2][64 lanes]
+    const int unit = wave & 3;
+    if (!is_b) {
 #pragma unroll
-    for (int h = 0; h < kHeadsPerWave; h++) {
-        const float inv_l = 1.0f / group_sum(l_run[h]);
-        uint16_t* out = a.out + static_cast<uint64_t>(my_tok) * a.q_stride + (h0 + h) * kHeadDim;
+        for (int h = 0; h < kHeadsPerWave; h++) {
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-            uint2 w;
-            w.x = pack2(o[h][dt][0] * inv_l, o[h][dt][1] * inv_l);
-            w.y = pack2(o[h][dt][2] * inv_l, o[h][dt][3] * inv_l);
-            *reinterpret_cast<uint2*>(out + 16 * dt + 4 * lg) = w;
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) xo[(((unit * kHeadsPerWave + h) * 8 + dt) * 4 + j) * 64 + lane] = o[h][dt][j];
+            xml[((unit * kHeadsPerWave + h) * 2 + 0) * 64 + lane] = m_run[h];
+            xml[((unit * kHeadsPerWave + h) * 2 + 1) * 64 + lane] = l_run[h];
         }
     }
+    __syncthreads();
+    if (!is_b) return;
+    const bool split = mid < n_b;   // the A waves computed B's chunks [mid, n_b)
+#pragma unroll
+    for (int h = 0; h < kHeadsPerWave; h++) {
+        float mb = m_run[h], lb = l_run[h];
+        if (split) {
+            const float ma = xml[((unit * kHeadsPerWave + h) * 2 + 0) * 64 + lane];
+            const float la = xml[((unit * kHeadsPerWave + h) * 2 + 1) * 64 + lane];
+            const float mm = fmaxf(mb, ma);
+            const float eb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - mm);
+            const float ea = ma == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ma - mm);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    o[h][dt][j] = o[h][dt][j] * eb + xo[(((unit * kHeadsPerWave + h) * 8 + dt) * 4 + j) * 64 + lane] * ea;
+            lb = lb * eb + la * ea;
+        }
+        l_run[h] = group_sum(lb);
+    }
+    write_unit();
 }
 
 }  // namespace

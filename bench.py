@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "prefill", "chunked"], default=None,
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "prefill", "chunked", "copy"], default=None,
                     help="run only one workload (for profiling)")
     return ap.parse_args()
 
@@ -89,14 +89,20 @@ class Bench:
 
 
 def time_region(torch, fn, steps, warmup):
+    """Seconds per fn() over `steps` calls after `warmup`, bracketed by
+    synchronizations and timed with HIP events recorded on the current stream
+    (the stream graph replays and the model's launches run on)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
     for _ in range(steps):
         fn()
+    end.record()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps
+    return start.elapsed_time(end) * 1e-3 / steps
 
 
 def per_launch_us(torch, b, launch, n_launch, replays=5):
@@ -203,6 +209,38 @@ def bench_prefill(torch, args, m, pos):
             "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS}
 
 
+def bench_copy(torch, args, nbytes=1 << 30):
+    """Plain device-to-device copy of a known size: the calibration for HBM
+    counters (FETCH_SIZE / WRITE_SIZE of this kernel vs nbytes read + written)
+    and the achievable-bandwidth reference."""
+    src = torch.ones(nbytes // 2, device="cuda", dtype=torch.float16)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    n = max(5, args.steps // 5)
+    start.record()
+    for _ in range(n):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / n
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "kernel_us_avg": us,
+            "GBps_read_plus_write": 2 * nbytes / (us * 1e-6) / 1e9}
+
+
+def measured_traffic(key):
+    """HBM bytes per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (scaled by a copy kernel of known size), from profiles/traffic.json."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)["bytes_per_dispatch"].get(key)
+
+
 def cpu_baseline(seconds=10.0):
     """CPU oracle (scalar C restatement of the reference's split/merge decode),
     1 thread, decode at ctx 4096 over as many layers as fit in ~seconds."""
@@ -239,6 +277,22 @@ def cpu_baseline(seconds=10.0):
                       "scalar C oracle restating attention_split + attention_merge"}
 
 
+def roofline_decode(d4):
+    """Dominant kernel pair of the headline step: decode_split_kernel<true> +
+    decode_merge_kernel<true>, i.e. one layer of the fused decode step.
+    achieved = algorithmic bytes of one layer (4097 rows x 2304 B + q in/out)
+    / the per-layer time of the timed region (HIP events, graph replays)."""
+    per_layer_s = d4["ms_per_step"] * 1e-3 / d4["layers"]
+    achieved = d4["kernel_bytes"] / per_layer_s / 1e9
+    split = measured_traffic("decode4k:decode_split_kernel<true>:32768")
+    merge = measured_traffic("decode4k:decode_merge_kernel<true>:8192")
+    traffic = None if split is None or merge is None else split + merge
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+            "kernel": "decode_split_kernel<true> + decode_merge_kernel<true> (one layer of the fused step)",
+            "bytes_per_launch": d4["kernel_bytes"], "us_per_launch": per_layer_s * 1e6}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -260,6 +314,8 @@ def main():
         extras["prefill_pp512"] = bench_prefill(torch, args, 512, 0)
     if args.only in (None, "chunked"):
         extras["chunked_prefill_2048_on_2048"] = bench_prefill(torch, args, 2048, 2048)
+    if args.only == "copy":
+        extras["copy_1GiB"] = bench_copy(torch, args)
     if args.only is not None:
         print(json.dumps(extras), flush=True)
         return
@@ -281,10 +337,7 @@ def main():
                                "(fused q_norm_rope + kv_writeback + split-K decode per layer, HIP graph)",
                    "n_head": 32, "n_kv_head": 8, "head_dim": 128, "ctx": 4096, "layers": 36,
                    "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "achieved": d4["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": d4["kernel_frac_hbm"], "traffic": None,
-                     "kernel": "decode_kernel", "bytes_per_launch": d4["kernel_bytes"],
-                     "us_per_launch": d4["kernel_us_avg"]},
+        "roofline": roofline_decode(d4),
         "cpu_baseline": cpu,
         **extras,
     }

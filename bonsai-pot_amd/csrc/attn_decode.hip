@@ -134,19 +134,44 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     const uint32_t n_rows = row_end - row0;
     const uint32_t n_batches =
         n_rows > 8u * wave ? (n_rows - 8u * wave + 32u * kRounds - 1) / (32u * kRounds) : 0u;
+    // ---- query-side loads first (unconditional): waiting for them below then
+    // leaves the first batch of rows in flight (loads retire in order). -----------
+    const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos) * kHeadDim + 2 * lane;
+    float qx0 = 0.f, qx1 = 0.f, w0 = 0.f, w1 = 0.f, c0 = 0.f, s0 = 0.f, x0 = 0.f, x1 = 0.f, kw0 = 0.f, kw1 = 0.f;
+    Q16 qraw[kGroup][2];
+    if constexpr (kFused) {
+        const uint16_t* qr = a.q + static_cast<uint64_t>(g * kGroup + wave) * kHeadDim;
+        qx0 = h2f(qr[lane]);
+        qx1 = h2f(qr[lane + 64]);
+        w0 = h2f(a.w_norms[a.w_q_off + lane]);
+        w1 = h2f(a.w_norms[a.w_q_off + lane + 64]);
+        c0 = h2f(cs[0]);
+        s0 = h2f(cs[1]);
+        const uint16_t* src = ((wave & 1) == 0 ? a.k_cur : a.v_cur) + g * kHeadDim;   // writeback input
+        x0 = h2f(src[lane]);
+        x1 = h2f(src[lane + 64]);
+        kw0 = h2f(a.w_norms[a.w_k_off + lane]);
+        kw1 = h2f(a.w_norms[a.w_k_off + lane + 64]);
+    } else {
+#pragma unroll
+        for (int h = 0; h < kGroup; h++) {
+            const uint16_t* qp = a.q + (static_cast<uint64_t>(g) * kGroup + h) * kHeadDim + 16 * seg;
+            qraw[h][0] = *reinterpret_cast<const Q16*>(qp);
+            qraw[h][1] = *reinterpret_cast<const Q16*>(qp + 8);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t last_b = n_batches > 0 ? n_batches - 1 : 0u;
     Batch A, Bb;
-    if (n_batches > 0) load(A, 0);   // first loads in flight before the query is read
+    load(A, 0);   // unconditional (clamped rows) so that every path has the same loads pending
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- the query slice of the 4 heads (as f16 pairs) ---------------------
-    const uint16_t* qsrc;
     if constexpr (kFused) {
         // q_norm_rope for head 4g + wave (q_norm_rope_fused.wgsl:38-96), into LDS.
         const uint32_t h = g * kGroup + wave;
-        const uint16_t* qr = a.q + static_cast<uint64_t>(h) * kHeadDim;
-        const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos) * kHeadDim + 2 * lane;
         float o0, o1;
-        norm_rope_pair(h2f(qr[lane]), h2f(qr[lane + 64]), h2f(a.w_norms[a.w_q_off + lane]),
-                       h2f(a.w_norms[a.w_q_off + lane + 64]), h2f(cs[0]), h2f(cs[1]), a.eps, o0, o1);
+        norm_rope_pair(qx0, qx1, w0, w1, c0, s0, a.eps, o0, o1);
         qn_sh[wave][lane] = f2h(o0);
         qn_sh[wave][lane + 64] = f2h(o1);
         if (split == 0) {
@@ -158,11 +183,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
             // wave 0 writes K (norm + RoPE + Q8_0), wave 1 writes V (Q8_0).
             const uint64_t d_idx = static_cast<uint64_t>(a.pos) * nb_row + g * (kHeadDim / kBlock);
             const uint64_t qs_idx = static_cast<uint64_t>(a.pos) * kv_dim + g * kHeadDim;
-            const uint16_t* src = (wave == 0 ? a.k_cur : a.v_cur) + g * kHeadDim;
-            float x0 = h2f(src[lane]), x1 = h2f(src[lane + 64]);
             if (wave == 0) {
-                norm_rope_pair(x0, x1, h2f(a.w_norms[a.w_k_off + lane]), h2f(a.w_norms[a.w_k_off + lane + 64]),
-                               h2f(cs[0]), h2f(cs[1]), a.eps, x0, x1);
+                norm_rope_pair(x0, x1, kw0, kw1, c0, s0, a.eps, x0, x1);
                 quantize_store_pair(x0, x1, lane, const_cast<float*>(a.k.d) + d_idx,
                                     const_cast<int8_t*>(a.k.qs) + qs_idx);
             } else {
@@ -171,22 +193,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
             }
         }
         __syncthreads();
-        qsrc = &qn_sh[0][0];
-    } else {
-        qsrc = a.q + static_cast<uint64_t>(g) * kGroup * kHeadDim;
+#pragma unroll
+        for (int h2i = 0; h2i < kGroup; h2i++) {
+            qraw[h2i][0] = *reinterpret_cast<const Q16*>(&qn_sh[h2i][16 * seg]);
+            qraw[h2i][1] = *reinterpret_cast<const Q16*>(&qn_sh[h2i][16 * seg + 8]);
+        }
     }
     h2 qh[kGroup][8];
     float qbias[kGroup];   // -1152 * sum(q) over this lane's 16 dims
 #pragma unroll
     for (int h = 0; h < kGroup; h++) {
-        const uint16_t* qp = qsrc + h * kHeadDim + 16 * seg;
-        const Q16 r0 = *reinterpret_cast<const Q16*>(qp);
-        const Q16 r1 = *reinterpret_cast<const Q16*>(qp + 8);
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            qh[h][i] = __builtin_bit_cast(h2, r0.w[i]);
-            qh[h][4 + i] = __builtin_bit_cast(h2, r1.w[i]);
+            qh[h][i] = __builtin_bit_cast(h2, qraw[h][0].w[i]);
+            qh[h][4 + i] = __builtin_bit_cast(h2, qraw[h][1].w[i]);
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) s += static_cast<float>(qh[h][i].x) + static_cast<float>(qh[h][i].y);
@@ -262,13 +283,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         }
     };
 
+    // Loads are unconditional (an index past the end re-reads the last batch,
+    // an L2 hit) so that each wait leaves the next batch in flight.
     if (n_batches > 0) {
         uint32_t b = 0;
         while (true) {
-            if (b + 1 < n_batches) load(Bb, b + 1);
+            load(Bb, min(b + 1, last_b));
+            __builtin_amdgcn_sched_barrier(0);
             consume(A, b);
             if (++b >= n_batches) break;
-            if (b + 1 < n_batches) load(A, b + 1);
+            load(A, min(b + 1, last_b));
+            __builtin_amdgcn_sched_barrier(0);
             consume(Bb, b);
             if (++b >= n_batches) break;
         }

@@ -236,7 +236,7 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
 
     m->kv_bytes = bp_kv_buffer_bytes(cfg->n_layer, m->kv_dim, max_seq);
     // Split-K partials: n_head x (at most decode_max_splits()) x stride floats.
-    m->decode_min_split_rows = 256;
+    m->decode_min_split_rows = 128;
     if (const char* env = std::getenv("BP_DECODE_MIN_SPLIT_ROWS")) {
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 32 && v <= (1 << 20)) m->decode_min_split_rows = static_cast<uint32_t>(v);

@@ -90,6 +90,12 @@ __device__ __forceinline__ float group_sum(float v) {
     return v + __shfl_xor(v, 32);
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// Two floats -> f16 pair with one packed round-to-nearest-even conversion.
+__device__ __forceinline__ uint32_t pack2_rne(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return static_cast<uint32_t>(f2h(a)) | (static_cast<uint32_t>(f2h(b)) << 16);
 }
@@ -125,6 +131,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     f16x8 qb[kHeadsPerWave][4];
     f32x4 o[kHeadsPerWave][8];
     float m_run[kHeadsPerWave], l_run[kHeadsPerWave];
+    f32x4 l_acc[kHeadsPerWave];   // row sums of P (every element holds the token's sum)
+    const f16x8 ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
     auto start_unit = [&](uint32_t tile) {
         wtok0 = tile * kPrefillTileTok + utok;
         my_tok = wtok0 + lr;
@@ -146,10 +154,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             for (int dt = 0; dt < 8; dt++) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
             m_run[h] = -INFINITY;
             l_run[h] = 0.0f;
+            l_acc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    // Normalize and store O (lane: token my_tok, dims 16dt + 4lg + j); l_run
-    // must already be summed over the token's 4 lane groups.
+    // Normalize and store O (lane: token my_tok, dims 16dt + 4lg + j) by l_run,
+    // the token's row sum.
     auto write_unit = [&]() {
         if (!unit_live || my_tok >= a.m_tokens) return;
 #pragma unroll
@@ -270,28 +279,27 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
                 const float m_new = up ? cm : m_run[h];
                 const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 from -inf
                 m_run[h] = m_new;
-                l_run[h] *= alpha;
+                l_acc[h][0] *= alpha;   // only element 0 is read
 #pragma unroll
                 for (int dt = 0; dt < 8; dt++) o[h][dt] *= alpha;
             }
             const float neg_m = -m_run[h];
-            float ps = 0.0f;
 #pragma unroll
             for (int kc = 0; kc < kSub / 2; kc++) {
                 float p[8];
 #pragma unroll
                 for (int half = 0; half < 2; half++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
+                    for (int j = 0; j < 4; j++)
                         p[4 * half + j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][2 * kc + half][j], c2, neg_m));
-                        ps += p[4 * half + j];
-                    }
                 U4 pk;
 #pragma unroll
-                for (int i = 0; i < 4; i++) pk.w[i] = pack2(p[2 * i], p[2 * i + 1]);
+                for (int i = 0; i < 4; i++) pk.w[i] = pack2_rne(p[2 * i], p[2 * i + 1]);
                 pb[h][kc] = __builtin_bit_cast(f16x8, pk);
+                // Row sum on the matrix core: ones x P^T sums the (rounded) P of
+                // each token over the 32 keys, in every row of the result.
+                l_acc[h] = mfma16(ones8, pb[h][kc], l_acc[h]);
             }
-            l_run[h] += ps;
         }
         // O^T += V^T P^T: per k-step 16 independent MFMAs.
 #pragma unroll
@@ -327,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
         if (on1 || has2(i)) compute(lds[on1 ? 0 : 1][buf], (on1 ? c1_of(i) : c2_of(i)) * kChunk);
         if (!is_b && i + 1 == n_a) {   // tile A done: store it, move to B's second half
 #pragma unroll
-            for (int h = 0; h < kHeadsPerWave; h++) l_run[h] = group_sum(l_run[h]);
+            for (int h = 0; h < kHeadsPerWave; h++) l_run[h] = l_acc[h][0];
             write_unit();
             start_unit(tile_b);
         }
@@ -349,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) xo[(((unit * kHeadsPerWave + h) * 8 + dt) * 4 + j) * 64 + lane] = o[h][dt][j];
             xml[((unit * kHeadsPerWave + h) * 2 + 0) * 64 + lane] = m_run[h];
-            xml[((unit * kHeadsPerWave + h) * 2 + 1) * 64 + lane] = l_run[h];
+            xml[((unit * kHeadsPerWave + h) * 2 + 1) * 64 + lane] = l_acc[h][0];
         }
     }
     __syncthreads();
@@ -357,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const bool split = mid < n_b;   // the A waves computed B's chunks [mid, n_b)
 #pragma unroll
     for (int h = 0; h < kHeadsPerWave; h++) {
-        float mb = m_run[h], lb = l_run[h];
+        float mb = m_run[h], lb = l_acc[h][0];
         if (split) {
             const float ma = xml[((unit * kHeadsPerWave + h) * 2 + 0) * 64 + lane];
             const float la = xml[((unit * kHeadsPerWave + h) * 2 + 1) * 64 + lane];
@@ -371,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
                     o[h][dt][j] = o[h][dt][j] * eb + xo[(((unit * kHeadsPerWave + h) * 8 + dt) * 4 + j) * 64 + lane] * ea;
             lb = lb * eb + la * ea;
         }
-        l_run[h] = group_sum(lb);
+        l_run[h] = lb;
     }
     write_unit();
 }

@@ -206,25 +206,44 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
         if (vr >= kend_b) S.vd0 = 0.0f;
         if (vr + 1 >= kend_b) S.vd1 = 0.0f;
     };
+    // Dequantization d * q -> f16: byte (q xor 0x80) under exponent byte 0x64
+    // is the exact f16 value x = 1152 + q (one v_perm per two values), and
+    // fma(x, d, -1152 d) = d * q (up to the f32 rounding of 1152 d) is rounded
+    // to f16 once by the mixed-precision FMA.
+    auto deq_pair = [&](uint32_t x, uint32_t sel, float d, float c) {
+        const f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, sel));
+        const f16x2 r = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.x), d, c)),
+                         static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.y), d, c))};
+        return __builtin_bit_cast(uint32_t, r);
+    };
     auto store_chunk = [&](const Stage& S, uint16_t* buf) {
         U4 lo, hi;
+        const float kc = -1152.0f * S.kd;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            lo.w[i] = pack2(S.kd * i8f(S.kq.w[i >> 1], 2 * (i & 1)), S.kd * i8f(S.kq.w[i >> 1], 2 * (i & 1) + 1));
-            hi.w[i] = pack2(S.kd * i8f(S.kq.w[2 + (i >> 1)], 2 * (i & 1)),
-                            S.kd * i8f(S.kq.w[2 + (i >> 1)], 2 * (i & 1) + 1));
+            const uint32_t x = S.kq.w[i] ^ 0x80808080u;   // dims 4i .. 4i+3 of the 16
+            const uint32_t p01 = deq_pair(x, 0x04010400u, S.kd, kc), p23 = deq_pair(x, 0x04030402u, S.kd, kc);
+            if (i < 2) { lo.w[2 * i] = p01; lo.w[2 * i + 1] = p23; }
+            else { hi.w[2 * i - 4] = p01; hi.w[2 * i - 3] = p23; }
         }
         uint16_t* kr = buf + krow * kKStride + 16 * kseg;
         *reinterpret_cast<U4*>(kr) = lo;
         *reinterpret_cast<U4*>(kr + 8) = hi;
         uint16_t* vb = buf + kKHalves;
         const int slot = v_slot(2 * vu);   // even; 2u + 1 sits in slot + 1
-        const uint32_t w0[2] = {S.v0.x, S.v0.y}, w1[2] = {S.v1.x, S.v1.y};
+        const float vc0 = -1152.0f * S.vd0, vc1 = -1152.0f * S.vd1;
+        const uint32_t w0[2] = {S.v0.x ^ 0x80808080u, S.v0.y ^ 0x80808080u};
+        const uint32_t w1[2] = {S.v1.x ^ 0x80808080u, S.v1.y ^ 0x80808080u};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int row = 8 * vdq + i;
-            *reinterpret_cast<uint32_t*>(vb + v_addr(row, slot)) =
-                pack2(S.vd0 * i8f(w0[i >> 2], i & 3), S.vd1 * i8f(w1[i >> 2], i & 3));
+            // rows 2u, 2u+1 of dim row: interleave their bytes, then one pair each
+            const uint32_t sel = 0x04000400u | (static_cast<uint32_t>(i & 3) << 16) | static_cast<uint32_t>(i & 3);
+            const f16x2 a0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w0[i >> 2], sel));
+            const f16x2 a1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w1[i >> 2], sel));
+            const f16x2 r = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(a0.x), S.vd0, vc0)),
+                             static_cast<_Float16>(__builtin_fmaf(static_cast<float>(a1.x), S.vd1, vc1))};
+            *reinterpret_cast<uint32_t*>(vb + v_addr(row, slot)) = __builtin_bit_cast(uint32_t, r);
         }
     };
 

@@ -231,14 +231,17 @@ def bench_copy(torch, args, nbytes=1 << 30):
             "GBps_read_plus_write": 2 * nbytes / (us * 1e-6) / 1e9}
 
 
-def measured_traffic(key):
-    """HBM bytes per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (scaled by a copy kernel of known size), from profiles/traffic.json."""
+def measured_traffic(workload, kernel):
+    """HBM bytes per dispatch of `kernel` in `workload`, measured with rocprofv3
+    FETCH_SIZE / WRITE_SIZE (scaled by a copy kernel of known size), from
+    profiles/traffic.json (keys "workload:kernel:grid")."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f)["bytes_per_dispatch"].get(key)
+        table = json.load(f)["bytes_per_dispatch"]
+    hits = [v for k, v in table.items() if k.startswith(f"{workload}:{kernel}:")]
+    return hits[0] if len(hits) == 1 else None
 
 
 def cpu_baseline(seconds=10.0):
@@ -284,8 +287,8 @@ def roofline_decode(d4):
     / the per-layer time of the timed region (HIP events, graph replays)."""
     per_layer_s = d4["ms_per_step"] * 1e-3 / d4["layers"]
     achieved = d4["kernel_bytes"] / per_layer_s / 1e9
-    split = measured_traffic("decode4k:decode_split_kernel<true>:32768")
-    merge = measured_traffic("decode4k:decode_merge_kernel<true>:8192")
+    split = measured_traffic("decode4k", "decode_split_kernel<true>")
+    merge = measured_traffic("decode4k", "decode_merge_kernel<true>")
     traffic = None if split is None or merge is None else split + merge
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,

@@ -47,7 +47,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kRounds = 4;                 // rounds (8 rows each) per wave batch
+constexpr int kRounds = 2;                 // rounds (8 rows each) per wave batch
 constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, pad (16-byte aligned rows)
 constexpr int kMaxSplits = 64;
 constexpr uint32_t kExp64 = 0x64646464u;

@@ -23,9 +23,10 @@
 //  * Online softmax in the exp2 domain; the batch max is shared by the whole
 //    wave, so running sums need no cross-lane reduction until the end and O
 //    is rescaled only when some max moved. Lane reductions use DPP / swizzle.
-//  * The 4 waves merge in LDS (log-sum-exp) into one partial (o[128], m, l)
-//    per query head, written with plain stores; with a single split the
-//    output is written directly and the merge pass is skipped.
+//  * O is summed over row-slot pairs with one DPP add and handed to LDS, where
+//    the 4 waves x 4 slot pairs are merged (log-sum-exp over the waves) into one
+//    partial (o[128], m, l) per query head, written with plain stores; with a
+//    single split the output is written directly and the merge pass is skipped.
 //
 // Merge pass (decode_merge_kernel) — one 64-lane workgroup per (query head,
 // 32-dim chunk): log-sum-exp over the splits (attention_merge.wgsl:85-129),
@@ -93,7 +94,9 @@ __device__ __forceinline__ float sum_slots(float v) {
 
 template <bool kFused>
 __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a) {
-    __shared__ float o_sh[kWaves][kGroup][kHeadDim];
+    // per wave and slot pair: O of the 4 heads (+4 pad: the pairs' rows start 4
+    // banks apart, so the 16-byte writes of a wave need the minimum 2 passes)
+    __shared__ __attribute__((aligned(16))) float o_red[kWaves][4][kGroup * kHeadDim + 4];
     __shared__ float ml_sh[kWaves][kGroup][2];
     __shared__ uint16_t qn_sh[kGroup][kHeadDim];
 
@@ -299,18 +302,25 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         }
     }
 
-    // ---- per-wave totals: O and l over the 8 row slots ---------------------
+    // ---- per-wave totals: l over the 8 row slots; O summed over slot pairs by
+    // one DPP add, then through LDS (the last two levels are done by the merge) --
 #pragma unroll
     for (int h = 0; h < kGroup; h++) {
         lsum[h] = sum_slots(lsum[h]);
 #pragma unroll
-        for (int i = 0; i < 16; i++) o[h][i] = sum_slots(o[h][i] - 128.0f * bsum[h]);
+        for (int i = 0; i < 16; i++) {
+            const float v = o[h][i] - 128.0f * bsum[h];
+            o[h][i] = v + dpp_f<0x128>(v);   // + row slot ^ 1 (row_ror:8 == xor 8 within 16 lanes)
+        }
     }
-    if (slot == 0) {
+    if ((slot & 1) == 0) {
+        float* dst = &o_red[wave][slot >> 1][16 * seg];
 #pragma unroll
         for (int h = 0; h < kGroup; h++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) o_sh[wave][h][16 * seg + i] = o[h][i];
+            for (int i = 0; i < 16; i += 4)
+                *reinterpret_cast<float4*>(dst + h * kHeadDim + i) =
+                    make_float4(o[h][i], o[h][i + 1], o[h][i + 2], o[h][i + 3]);
     }
     if (lane == 0) {
 #pragma unroll
@@ -318,7 +328,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     }
     __syncthreads();
 
-    // ---- merge the 4 waves; thread t -> head t>>6, dims 2*(t&63), +1 -------
+    // ---- merge the 4 waves x 4 slot pairs; thread t -> head t>>6, dims 2*(t&63), +1 --
     const int fh = t >> 6, fd = 2 * (t & 63);
     float M = -INFINITY;
 #pragma unroll
@@ -329,8 +339,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         const float mw = ml_sh[w][fh][0];
         const float e = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);   // waves without rows
         L = __builtin_fmaf(e, ml_sh[w][fh][1], L);
-        o0 = __builtin_fmaf(e, o_sh[w][fh][fd], o0);
-        o1 = __builtin_fmaf(e, o_sh[w][fh][fd + 1], o1);
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int pr = 0; pr < 4; pr++) {
+            const float2 v = *reinterpret_cast<const float2*>(&o_red[w][pr][fh * kHeadDim + fd]);
+            s0 += v.x;
+            s1 += v.y;
+        }
+        o0 = __builtin_fmaf(e, s0, o0);
+        o1 = __builtin_fmaf(e, s1, o1);
     }
     const uint32_t qhd = g * kGroup + fh;
     if (!kFused && a.n_splits == 1) {

@@ -45,6 +45,9 @@ namespace bp {
 namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
@@ -57,9 +60,21 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct alignas(16) Q16 { uint32_t w[4]; };
 
 struct Batch {
-    Q16 kq[kRounds], vq[kRounds];
+    Q16 kq[kRounds];           // q.k role: 16 bytes of row (8r + slot)
     float kd[kRounds], vd[kRounds];
+    u32x2 vv[4];               // p.v role: dims 8 lr .. +8 of rows 4 lg + j
 };
+
+__device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// Pick element i (0..3) of a 4-vector with a non-uniform i.
+__device__ __forceinline__ float pick4(f32x4 v, int i) {
+    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
+__device__ __forceinline__ float pick4(const float (&v)[4], int i) {
+    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
 
 __device__ __forceinline__ float ub(uint32_t w, int i) {   // v_cvt_f32_ubyte{i}
     return static_cast<float>((w >> (8 * i)) & 0xffu);
@@ -94,9 +109,8 @@ __device__ __forceinline__ float sum_slots(float v) {
 
 template <bool kFused>
 __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a) {
-    // per wave and slot pair: O of the 4 heads (+4 pad: the pairs' rows start 4
-    // banks apart, so the 16-byte writes of a wave need the minimum 2 passes)
-    __shared__ __attribute__((aligned(16))) float o_red[kWaves][4][kGroup * kHeadDim + 4];
+    __shared__ __attribute__((aligned(16))) float o_red[kWaves][kGroup][kHeadDim + 4];   // per-wave O
+    __shared__ __attribute__((aligned(16))) float w_sh[kWaves][4][kGroup][16];           // W: [block][head][row]
     __shared__ float ml_sh[kWaves][kGroup][2];
     __shared__ uint16_t qn_sh[kGroup][kHeadDim];
 
@@ -104,6 +118,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     const int lane = t & 63, wave = t >> 6;
     const int seg = lane & 7;              // dims [16*seg, 16*seg+16)
     const int slot = lane >> 3;            // row within a round
+    const int lr = lane & 15, lg = lane >> 4;   // p.v role: column (head lr>>2, block lr&3), rows 4 lg ..
     // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
     // linear id, so ids are laid out as [split / 8][g][split % 8] — the KV
     // heads of one split share an XCD and hence its L2 copy of the rows' FP32
@@ -121,8 +136,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     const uint32_t nb_row = a.kv_dim / kBlock;
     const uint32_t col = g * kHeadDim + 16 * seg;
     const uint32_t dcol = g * (kHeadDim / kBlock) + (seg >> 1);
+    // A wave's batch is 16 consecutive rows (the workgroup's 4 waves cover 64).
     auto row_of = [&](uint32_t b, int r) {
-        return row0 + 32u * (kRounds * b + r) + 8u * wave + slot;
+        return row0 + 64u * b + 16u * wave + 8u * r + slot;
     };
     auto load = [&](Batch& B, uint32_t b) {
 #pragma unroll
@@ -130,13 +146,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
             const uint64_t row = min(row_of(b, r), row_end - 1);
             B.kq[r] = *reinterpret_cast<const Q16*>(a.k.qs + row * kv_dim + col);
             B.kd[r] = a.k.d[row * nb_row + dcol];
-            B.vq[r] = *reinterpret_cast<const Q16*>(a.v.qs + row * kv_dim + col);
             B.vd[r] = a.v.d[row * nb_row + dcol];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint64_t vr = min(row0 + 64u * b + 16u * wave + 4u * lg + j, row_end - 1);
+            B.vv[j] = *reinterpret_cast<const u32x2*>(a.v.qs + vr * kv_dim + g * kHeadDim + 8 * lr);
         }
     };
     const uint32_t n_rows = row_end - row0;
-    const uint32_t n_batches =
-        n_rows > 8u * wave ? (n_rows - 8u * wave + 32u * kRounds - 1) / (32u * kRounds) : 0u;
+    const uint32_t n_batches = n_rows > 16u * wave ? (n_rows - 16u * wave + 63u) / 64u : 0u;
     // ---- query-side loads first (unconditional): waiting for them below then
     // leaves the first batch of rows in flight (loads retire in order). -----------
     const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos) * kHeadDim + 2 * lane;
@@ -217,13 +236,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         qbias[h] = -1152.0f * s;
     }
 
-    float o[kGroup][16], bsum[kGroup], lsum[kGroup], m_run[kGroup];
+    float lsum[kGroup], m_run[kGroup];
 #pragma unroll
-    for (int h = 0; h < kGroup; h++) {
-        bsum[h] = 0.0f; lsum[h] = 0.0f; m_run[h] = -INFINITY;
+    for (int h = 0; h < kGroup; h++) { lsum[h] = 0.0f; m_run[h] = -INFINITY; }
+    // p.v state: O^T tiles (lane holds rows (h = lg, b = j) x dim 8 lr + tt; the
+    // kept entry is j = lr >> 2, the block of those dims) and the column sum of W.
+    f32x4 oacc[8];
 #pragma unroll
-        for (int i = 0; i < 16; i++) o[h][i] = 0.0f;
-    }
+    for (int i = 0; i < 8; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float bsum = 0.0f;
+    const int ch = lr >> 2, cb = lr & 3;
+    const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
     auto consume = [&](const Batch& B, uint32_t b) {
         float s[kRounds][kGroup];
@@ -261,29 +284,65 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         }
         if (moved) {   // wave-uniform: m_run is identical in all lanes
 #pragma unroll
-            for (int h = 0; h < kGroup; h++) {
-                lsum[h] *= alpha[h];
-                bsum[h] *= alpha[h];
+            for (int h = 0; h < kGroup; h++) lsum[h] *= alpha[h];
+            bsum *= pick4(alpha, ch);
+            const float ao = pick4(alpha, lg);
 #pragma unroll
-                for (int i = 0; i < 16; i++) o[h][i] *= alpha[h];
-            }
+            for (int i = 0; i < 8; i++) oacc[i] *= ao;
         }
+        // W = p * d_v: the q.k lanes of block (seg >> 1) publish their row's
+        // weights (0 for masked rows, which repeat a real, finite row).
 #pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            float vf[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++) vf[i] = ub(B.vq[r].w[i >> 2] ^ 0x80808080u, i & 3);
+        for (int r = 0; r < kRounds; r++)
 #pragma unroll
             for (int h = 0; h < kGroup; h++) {
-                // 0 for masked rows, which repeat a real, finite row: p * v stays 0
                 const float p = __builtin_amdgcn_exp2f(s[r][h] - m_run[h]);
                 lsum[h] += p;
-                const float pv = p * B.vd[r];
-                bsum[h] += pv;
+                if ((seg & 1) == 0) w_sh[wave][seg >> 1][h][8 * r + slot] = p * B.vd[r];
+            }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();
+        // A operand (W^T row (ch, cb), rows 4 lg .. +3) as two f16 terms.
+        const float4 wv = *reinterpret_cast<const float4*>(&w_sh[wave][cb][ch][4 * lg]);
+        const float wf[4] = {wv.x, wv.y, wv.z, wv.w};
+        f16x4 whi, wlo;
 #pragma unroll
-                for (int i = 0; i < 16; i++) o[h][i] = __builtin_fmaf(pv, vf[i], o[h][i]);
+        for (int j = 0; j < 4; j++) {
+            whi[j] = static_cast<_Float16>(wf[j]);
+            wlo[j] = static_cast<_Float16>(wf[j] - static_cast<float>(whi[j]));
+        }
+        bsum = __builtin_amdgcn_fdot2(h2{whi[0], whi[1]}, ones, bsum, false);
+        bsum = __builtin_amdgcn_fdot2(h2{whi[2], whi[3]}, ones, bsum, false);
+        bsum = __builtin_amdgcn_fdot2(h2{wlo[0], wlo[1]}, ones, bsum, false);
+        bsum = __builtin_amdgcn_fdot2(h2{wlo[2], wlo[3]}, ones, bsum, false);
+        // B operand per output tile tt (dim 8 lr + tt): the 4 rows' bytes of
+        // that dim, byte-transposed, as exact f16 values 1152 + v.
+        uint32_t rw[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            rw[j][0] = B.vv[j].x ^ 0x80808080u;
+            rw[j][1] = B.vv[j].y ^ 0x80808080u;
+        }
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const uint32_t t01l = __builtin_amdgcn_perm(rw[1][hf], rw[0][hf], 0x05010400u);   // r0b0 r1b0 r0b1 r1b1
+            const uint32_t t01h = __builtin_amdgcn_perm(rw[1][hf], rw[0][hf], 0x07030602u);   // r0b2 r1b2 r0b3 r1b3
+            const uint32_t t23l = __builtin_amdgcn_perm(rw[3][hf], rw[2][hf], 0x05010400u);
+            const uint32_t t23h = __builtin_amdgcn_perm(rw[3][hf], rw[2][hf], 0x07030602u);
+            const uint32_t src01[4] = {t01l, t01l, t01h, t01h};
+            const uint32_t src23[4] = {t23l, t23l, t23h, t23h};
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const uint32_t sel = (d & 1) ? 0x04030402u : 0x04010400u;
+                const u32x2 bv = {__builtin_amdgcn_perm(kExp64, src01[d], sel), __builtin_amdgcn_perm(kExp64, src23[d], sel)};
+                const f16x4 bop = __builtin_bit_cast(f16x4, bv);
+                const int tt = 4 * hf + d;
+                oacc[tt] = mfma16(whi, bop, oacc[tt]);
+                oacc[tt] = mfma16(wlo, bop, oacc[tt]);
             }
         }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();
     };
 
     // Loads are unconditional (an index past the end re-reads the last batch,
@@ -302,25 +361,20 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         }
     }
 
-    // ---- per-wave totals: l over the 8 row slots; O summed over slot pairs by
-    // one DPP add, then through LDS (the last two levels are done by the merge) --
+    // ---- per-wave totals: l over the 8 row slots; O of head lg, dims 8 lr .. +8
+    // minus the 1152 bias of V (the column sum of W over all rows) ----------------
 #pragma unroll
-    for (int h = 0; h < kGroup; h++) {
-        lsum[h] = sum_slots(lsum[h]);
+    for (int h = 0; h < kGroup; h++) lsum[h] = sum_slots(lsum[h]);
+    float bs = bsum + swz_xor16(bsum);
+    bs += __shfl_xor(bs, 32);
+    const float bias = 1152.0f * __shfl(bs, 4 * lg + (lr >> 2));
+    {
+        float ov[8];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float v = o[h][i] - 128.0f * bsum[h];
-            o[h][i] = v + dpp_f<0x128>(v);   // + row slot ^ 1 (row_ror:8 == xor 8 within 16 lanes)
-        }
-    }
-    if ((slot & 1) == 0) {
-        float* dst = &o_red[wave][slot >> 1][16 * seg];
-#pragma unroll
-        for (int h = 0; h < kGroup; h++)
-#pragma unroll
-            for (int i = 0; i < 16; i += 4)
-                *reinterpret_cast<float4*>(dst + h * kHeadDim + i) =
-                    make_float4(o[h][i], o[h][i + 1], o[h][i + 2], o[h][i + 3]);
+        for (int tt = 0; tt < 8; tt++) ov[tt] = pick4(oacc[tt], lr >> 2) - bias;
+        float* dst = &o_red[wave][lg][8 * lr];
+        *reinterpret_cast<float4*>(dst) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(ov[4], ov[5], ov[6], ov[7]);
     }
     if (lane == 0) {
 #pragma unroll
@@ -328,7 +382,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     }
     __syncthreads();
 
-    // ---- merge the 4 waves x 4 slot pairs; thread t -> head t>>6, dims 2*(t&63), +1 --
+    // ---- merge the 4 waves; thread t -> head t>>6, dims 2*(t&63), +1 -----------
     const int fh = t >> 6, fd = 2 * (t & 63);
     float M = -INFINITY;
 #pragma unroll
@@ -339,15 +393,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         const float mw = ml_sh[w][fh][0];
         const float e = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);   // waves without rows
         L = __builtin_fmaf(e, ml_sh[w][fh][1], L);
-        float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-        for (int pr = 0; pr < 4; pr++) {
-            const float2 v = *reinterpret_cast<const float2*>(&o_red[w][pr][fh * kHeadDim + fd]);
-            s0 += v.x;
-            s1 += v.y;
-        }
-        o0 = __builtin_fmaf(e, s0, o0);
-        o1 = __builtin_fmaf(e, s1, o1);
+        const float2 v = *reinterpret_cast<const float2*>(&o_red[w][fh][fd]);
+        o0 = __builtin_fmaf(e, v.x, o0);
+        o1 = __builtin_fmaf(e, v.y, o1);
     }
     const uint32_t qhd = g * kGroup + fh;
     if (!kFused && a.n_splits == 1) {
@@ -440,14 +488,14 @@ void decode_plan(uint32_t n_rows, uint32_t n_kv_head, int cu_count, uint32_t min
                  uint32_t* split_len, uint32_t* n_splits) {
     // Enough workgroups to cover the CUs twice, but at least min_split_rows
     // rows each (fewer partials at short context) and at most kMaxSplits
-    // splits; rows per split are a multiple of 32 (one round of all 4 waves).
+    // splits; rows per split are a multiple of 64 (one batch of all 4 waves).
     const uint32_t target = static_cast<uint32_t>(cu_count > 0 ? cu_count : 256) * 2;
     uint32_t want = (target + n_kv_head - 1) / n_kv_head;
     if (want < 1) want = 1;
     if (want > kMaxSplits) want = kMaxSplits;
     uint32_t len = (n_rows + want - 1) / want;
     if (len < min_split_rows) len = min_split_rows;
-    len = (len + 31) / 32 * 32;
+    len = (len + 63) / 64 * 64;
     *split_len = len;
     *n_splits = n_rows == 0 ? 1 : (n_rows + len - 1) / len;
 }

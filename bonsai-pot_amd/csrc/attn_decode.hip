@@ -432,17 +432,27 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
     const float m_s = static_cast<uint32_t>(lane) < ns ? ml.x : -INFINITY;
 
     float s_new = -INFINITY;   // log2-domain score of the new row (fused step)
+    // Row `pos` of V for dims d0 .. d0 + 3 (lanes 0-7 use it), loaded up front with
+    // everything else so that the pass has a single memory round trip.
+    const uint32_t d0 = 32 * c + 4 * f4;
+    float vd_new = 0.0f;
+    uint32_t vq_new = 0;
     if constexpr (kFused) {
-        const uint16_t* qn = a.q_norm + static_cast<uint64_t>(h) * kHeadDim;
-        const float q0 = h2f(qn[lane]), q1 = h2f(qn[lane + 64]);
         const uint64_t row = a.pos;
         const uint32_t nb_row = a.kv_dim / kBlock;
+        const uint16_t* qn = a.q_norm + static_cast<uint64_t>(h) * kHeadDim;
         const float* kd = a.k.d + row * nb_row + g * (kHeadDim / kBlock);
         const int8_t* kq = a.k.qs + row * a.kv_dim + g * kHeadDim;
+        vd_new = a.v.d[row * nb_row + g * (kHeadDim / kBlock) + (d0 >> 5)];
+        vq_new = *reinterpret_cast<const uint32_t*>(a.v.qs + row * a.kv_dim + g * kHeadDim + d0);
+        const uint16_t qa = qn[lane], qb = qn[lane + 64];
+        const float q0 = h2f(qa), q1 = h2f(qb);
         const float k0 = kd[lane >> 5] * static_cast<float>(kq[lane]);
         const float k1 = kd[2 + (lane >> 5)] * static_cast<float>(kq[lane + 64]);
         s_new = wave_sum(q0 * k0 + q1 * k1) * c2;
-        if (lane < 32) a.q_act[h * kHeadDim + 32 * c + lane] = qn[32 * c + lane];   // q_norm_rope output
+        // q_norm_rope output: element 32 c + lane, already in a register of this wave.
+        const uint16_t qv = static_cast<uint16_t>(__shfl(static_cast<int>(c < 2 ? qa : qb), static_cast<int>((32 * c + lane) & 63)));
+        if (lane < 32) a.q_act[h * kHeadDim + 32 * c + lane] = qv;
     }
     const float M = fmaxf(wave_max(m_s), s_new);
     const float w = m_s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s - M);
@@ -463,16 +473,12 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
     acc.z = sum_slots(acc.z);
     acc.w = sum_slots(acc.w);
     if (lane < 8) {
-        const uint32_t d0 = 32 * c + 4 * f4;
         if constexpr (kFused) {
-            const uint64_t row = a.pos;
-            const uint32_t nb_row = a.kv_dim / kBlock;
-            const float vd = a.v.d[row * nb_row + g * (kHeadDim / kBlock) + (d0 >> 5)];
-            const int8_t* vq = a.v.qs + row * a.kv_dim + g * kHeadDim + d0;
-            acc.x = __builtin_fmaf(w_new, vd * static_cast<float>(vq[0]), acc.x);
-            acc.y = __builtin_fmaf(w_new, vd * static_cast<float>(vq[1]), acc.y);
-            acc.z = __builtin_fmaf(w_new, vd * static_cast<float>(vq[2]), acc.z);
-            acc.w = __builtin_fmaf(w_new, vd * static_cast<float>(vq[3]), acc.w);
+            const float vd = vd_new;
+            acc.x = __builtin_fmaf(w_new, vd * static_cast<float>(static_cast<int8_t>(vq_new)), acc.x);
+            acc.y = __builtin_fmaf(w_new, vd * static_cast<float>(static_cast<int8_t>(vq_new >> 8)), acc.y);
+            acc.z = __builtin_fmaf(w_new, vd * static_cast<float>(static_cast<int8_t>(vq_new >> 16)), acc.z);
+            acc.w = __builtin_fmaf(w_new, vd * static_cast<float>(static_cast<int8_t>(vq_new >> 24)), acc.w);
         }
         const float inv_l = 1.0f / L;
         uint2 o;

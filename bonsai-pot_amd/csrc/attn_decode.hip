@@ -48,6 +48,8 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
@@ -60,10 +62,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct alignas(16) Q16 { uint32_t w[4]; };
 
 struct Batch {
-    Q16 kq[kRounds];           // q.k role: 16 bytes of row (8r + slot)
-    float kd[kRounds], vd[kRounds];
-    u32x2 vv[4];               // p.v role: dims 8 lr .. +8 of rows 4 lg + j
+    Q16 kq[2];        // q.k: the 32 bytes of block lg of row lr
+    f32x4 kd, vd;     // scales of block (lr & 3) of rows 4 lg + j
+    u32x2 vv[4];      // p.v: dims 8 lr .. +8 of rows 4 lg + j
 };
+
+__device__ __forceinline__ f32x4 mfma32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -110,15 +116,18 @@ __device__ __forceinline__ float sum_slots(float v) {
 template <bool kFused>
 __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a) {
     __shared__ __attribute__((aligned(16))) float o_red[kWaves][kGroup][kHeadDim + 4];   // per-wave O
-    __shared__ __attribute__((aligned(16))) float w_sh[kWaves][4][kGroup][16];           // W: [block][head][row]
     __shared__ float ml_sh[kWaves][kGroup][2];
-    __shared__ uint16_t qn_sh[kGroup][kHeadDim];
+    __shared__ __attribute__((aligned(16))) uint16_t qn_sh[kGroup][kHeadDim];
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
-    const int seg = lane & 7;              // dims [16*seg, 16*seg+16)
-    const int slot = lane >> 3;            // row within a round
-    const int lr = lane & 15, lg = lane >> 4;   // p.v role: column (head lr>>2, block lr&3), rows 4 lg ..
+    // Lane roles, all from (lr, lg) = (lane & 15, lane >> 4):
+    //  q.k   A = K rows (m = row lr), B = q masked per block (n = lr = 4 h + b),
+    //        so D lane holds the block-b partial dot of head h for rows 4 lg + j;
+    //  p.v   A = W^T (m = lr = (h, b), rows 4 lg + j), B = V (n = dims, rows 4 lg + j),
+    //        D lane holds O^T rows (head lg, block j) at dims (tile, lr).
+    const int lr = lane & 15, lg = lane >> 4;
+    const int hq = lr >> 2, bq = lr & 3;   // the (head, block) column of this lane
     // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
     // linear id, so ids are laid out as [split / 8][g][split % 8] — the KV
     // heads of one split share an XCD and hence its L2 copy of the rows' FP32
@@ -132,26 +141,23 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     const uint32_t row_end = min(row0 + a.split_len, a.n_rows);
     const float c2 = a.scale * kLog2e;   // scores in log2 units
 
-    const uint64_t kv_dim = a.kv_dim;
+    const uint32_t kv_dim = a.kv_dim;
     const uint32_t nb_row = a.kv_dim / kBlock;
-    const uint32_t col = g * kHeadDim + 16 * seg;
-    const uint32_t dcol = g * (kHeadDim / kBlock) + (seg >> 1);
-    // A wave's batch is 16 consecutive rows (the workgroup's 4 waves cover 64).
-    auto row_of = [&](uint32_t b, int r) {
-        return row0 + 64u * b + 16u * wave + 8u * r + slot;
-    };
+    // 32-bit offsets from the layer bases (a layer's section is < 4 GiB).
+    const uint32_t kcol = g * kHeadDim + 32 * lg;          // q.k: block lg
+    const uint32_t vcol = g * kHeadDim + 8 * lr;           // p.v: dims 8 lr .. +8
+    const uint32_t dcol = g * (kHeadDim / kBlock) + bq;    // scale of block bq
     auto load = [&](Batch& B, uint32_t b) {
-#pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            const uint64_t row = min(row_of(b, r), row_end - 1);
-            B.kq[r] = *reinterpret_cast<const Q16*>(a.k.qs + row * kv_dim + col);
-            B.kd[r] = a.k.d[row * nb_row + dcol];
-            B.vd[r] = a.v.d[row * nb_row + dcol];
-        }
+        const uint32_t r0 = row0 + 64u * b + 16u * wave;
+        const uint32_t rk = min(r0 + lr, row_end - 1);
+        B.kq[0] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol));
+        B.kq[1] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol + 16));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint64_t vr = min(row0 + 64u * b + 16u * wave + 4u * lg + j, row_end - 1);
-            B.vv[j] = *reinterpret_cast<const u32x2*>(a.v.qs + vr * kv_dim + g * kHeadDim + 8 * lr);
+            const uint32_t rr = min(r0 + 4u * lg + j, row_end - 1);
+            B.kd[j] = a.k.d[rr * nb_row + dcol];
+            B.vd[j] = a.v.d[rr * nb_row + dcol];
+            B.vv[j] = *reinterpret_cast<const u32x2*>(a.v.qs + (rr * kv_dim + vcol));
         }
     };
     const uint32_t n_rows = row_end - row0;
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     // leaves the first batch of rows in flight (loads retire in order). -----------
     const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos) * kHeadDim + 2 * lane;
     float qx0 = 0.f, qx1 = 0.f, w0 = 0.f, w1 = 0.f, c0 = 0.f, s0 = 0.f, x0 = 0.f, x1 = 0.f, kw0 = 0.f, kw1 = 0.f;
-    Q16 qraw[kGroup][2];
+    Q16 qraw[4];   // q of head hq, dims 32 lg + 8 i .. +8
     if constexpr (kFused) {
         const uint16_t* qr = a.q + static_cast<uint64_t>(g * kGroup + wave) * kHeadDim;
         qx0 = h2f(qr[lane]);
@@ -175,12 +181,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         kw0 = h2f(a.w_norms[a.w_k_off + lane]);
         kw1 = h2f(a.w_norms[a.w_k_off + lane + 64]);
     } else {
+        const uint16_t* qp = a.q + (static_cast<uint64_t>(g) * kGroup + hq) * kHeadDim + 32 * lg;
 #pragma unroll
-        for (int h = 0; h < kGroup; h++) {
-            const uint16_t* qp = a.q + (static_cast<uint64_t>(g) * kGroup + h) * kHeadDim + 16 * seg;
-            qraw[h][0] = *reinterpret_cast<const Q16*>(qp);
-            qraw[h][1] = *reinterpret_cast<const Q16*>(qp + 8);
-        }
+        for (int i = 0; i < 4; i++) qraw[i] = *reinterpret_cast<const Q16*>(qp + 8 * i);
     }
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t last_b = n_batches > 0 ? n_batches - 1 : 0u;
@@ -188,7 +191,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     load(A, 0);   // unconditional (clamped rows) so that every path has the same loads pending
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- the query slice of the 4 heads (as f16 pairs) ---------------------
     if constexpr (kFused) {
         // q_norm_rope for head 4g + wave (q_norm_rope_fused.wgsl:38-96), into LDS.
         const uint32_t h = g * kGroup + wave;
@@ -216,100 +218,80 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         }
         __syncthreads();
 #pragma unroll
-        for (int h2i = 0; h2i < kGroup; h2i++) {
-            qraw[h2i][0] = *reinterpret_cast<const Q16*>(&qn_sh[h2i][16 * seg]);
-            qraw[h2i][1] = *reinterpret_cast<const Q16*>(&qn_sh[h2i][16 * seg + 8]);
-        }
+        for (int i = 0; i < 4; i++) qraw[i] = *reinterpret_cast<const Q16*>(&qn_sh[hq][32 * lg + 8 * i]);
     }
-    h2 qh[kGroup][8];
-    float qbias[kGroup];   // -1152 * sum(q) over this lane's 16 dims
+    // ---- B operand of q.k: q of head hq on block bq's k slots, zero elsewhere;
+    // and the bias 1152 * sum(q over block bq) of the exact-f16 K trick. -----------
+    f16x8 qop[4];
+    float qsum = 0.0f;
 #pragma unroll
-    for (int h = 0; h < kGroup; h++) {
-        float s = 0.0f;
+    for (int i = 0; i < 4; i++) {
+        const f16x8 v = __builtin_bit_cast(f16x8, qraw[i]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            qh[h][i] = __builtin_bit_cast(h2, qraw[h][0].w[i]);
-            qh[h][4 + i] = __builtin_bit_cast(h2, qraw[h][1].w[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++) s += static_cast<float>(qh[h][i].x) + static_cast<float>(qh[h][i].y);
-        qbias[h] = -1152.0f * s;
+        for (int e = 0; e < 8; e++) qsum += static_cast<float>(v[e]);
+        qop[i] = lg == bq ? v : f16x8{};
     }
+    const float qb = 1152.0f * __shfl(qsum, lr + 16 * bq);   // from the lane holding block bq
 
-    float lsum[kGroup], m_run[kGroup];
-#pragma unroll
-    for (int h = 0; h < kGroup; h++) { lsum[h] = 0.0f; m_run[h] = -INFINITY; }
-    // p.v state: O^T tiles (lane holds rows (h = lg, b = j) x dim 8 lr + tt; the
-    // kept entry is j = lr >> 2, the block of those dims) and the column sum of W.
+    float lsum = 0.0f, m_run = -INFINITY;   // of head hq, unscaled score units
     f32x4 oacc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float bsum = 0.0f;
-    const int ch = lr >> 2, cb = lr & 3;
+    float bsum = 0.0f;   // column (hq, bq) sum of W, for the 1152 bias of V
     const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
-    auto consume = [&](const Batch& B, uint32_t b) {
-        float s[kRounds][kGroup];
+    auto consume = [&](const Batch& B, uint32_t b, bool tail) {
+        // q.k on the matrix core: 4 MFMAs over the 32 bytes of block lg of row lr.
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            h2 kh[8];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t x = B.kq[r].w[i] ^ 0x80808080u;
-                kh[2 * i] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kExp64, x, 0x04010400u));
-                kh[2 * i + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(kExp64, x, 0x04030402u));
-            }
-            const bool ok = row_of(b, r) < row_end;
-#pragma unroll
-            for (int h = 0; h < kGroup; h++) {
-                float acc = qbias[h];
-#pragma unroll
-                for (int i = 0; i < 8; i++) acc = __builtin_amdgcn_fdot2(qh[h][i], kh[i], acc, false);
-                const float dot = sum8(acc * B.kd[r]);
-                s[r][h] = ok ? dot * c2 : -INFINITY;
-            }
+        for (int i = 0; i < 4; i++) {
+            const uint32_t x = B.kq[i >> 1].w[2 * (i & 1)] ^ 0x80808080u;
+            const uint32_t y = B.kq[i >> 1].w[2 * (i & 1) + 1] ^ 0x80808080u;
+            const u32x4 kw = {__builtin_amdgcn_perm(kExp64, x, 0x04010400u), __builtin_amdgcn_perm(kExp64, x, 0x04030402u),
+                              __builtin_amdgcn_perm(kExp64, y, 0x04010400u), __builtin_amdgcn_perm(kExp64, y, 0x04030402u)};
+            d = mfma32(__builtin_bit_cast(f16x8, kw), qop[i], d);
         }
-        float alpha[kGroup];
-        bool moved = false;
+        // s(row 4 lg + j, head hq) = sum over the 4 blocks (the lane quad) of d_b * (D - bias).
+        float s[4];
 #pragma unroll
-        for (int h = 0; h < kGroup; h++) {
-            float bm = s[0][h];
-#pragma unroll
-            for (int r = 1; r < kRounds; r++) bm = fmaxf(bm, s[r][h]);
-            bm = max_slots(bm);
-            const float m_new = fmaxf(m_run[h], bm);
-            alpha[h] = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 on the first batch
-            moved |= m_new != m_run[h];
-            m_run[h] = m_new;
+        for (int j = 0; j < 4; j++) {
+            float v = B.kd[j] * (d[j] - qb);
+            v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+            v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+            s[j] = v;
         }
-        if (moved) {   // wave-uniform: m_run is identical in all lanes
+        if (tail) {
+            const uint32_t r0 = row0 + 64u * b + 16u * wave + 4u * lg;
 #pragma unroll
-            for (int h = 0; h < kGroup; h++) lsum[h] *= alpha[h];
-            bsum *= pick4(alpha, ch);
-            const float ao = pick4(alpha, lg);
+            for (int j = 0; j < 4; j++) s[j] = r0 + j < row_end ? s[j] : -INFINITY;
+        }
+        float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        bm = fmaxf(bm, swz_xor16(bm));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float m_new = fmaxf(m_run, bm);
+        if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);   // 0 on the first batch
+            lsum *= alpha;
+            bsum *= alpha;
+            const float ao = __shfl(alpha, 4 * lg);   // head lg
 #pragma unroll
             for (int i = 0; i < 8; i++) oacc[i] *= ao;
+            m_run = m_new;
         }
-        // W = p * d_v: the q.k lanes of block (seg >> 1) publish their row's
-        // weights (0 for masked rows, which repeat a real, finite row).
+        const float mc = m_run * c2;
+        float w[4];
 #pragma unroll
-        for (int r = 0; r < kRounds; r++)
-#pragma unroll
-            for (int h = 0; h < kGroup; h++) {
-                const float p = __builtin_amdgcn_exp2f(s[r][h] - m_run[h]);
-                lsum[h] += p;
-                if ((seg & 1) == 0) w_sh[wave][seg >> 1][h][8 * r + slot] = p * B.vd[r];
-            }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_wave_barrier();
-        // A operand (W^T row (ch, cb), rows 4 lg .. +3) as two f16 terms.
-        const float4 wv = *reinterpret_cast<const float4*>(&w_sh[wave][cb][ch][4 * lg]);
-        const float wf[4] = {wv.x, wv.y, wv.z, wv.w};
+        for (int j = 0; j < 4; j++) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], c2, -mc));
+            lsum += p;
+            w[j] = p * B.vd[j];
+        }
+        // A operand (W^T row (hq, bq), rows 4 lg + j) as two f16 terms.
         f16x4 whi, wlo;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            whi[j] = static_cast<_Float16>(wf[j]);
-            wlo[j] = static_cast<_Float16>(wf[j] - static_cast<float>(whi[j]));
+            whi[j] = static_cast<_Float16>(w[j]);
+            wlo[j] = static_cast<_Float16>(w[j] - static_cast<float>(whi[j]));
         }
         bsum = __builtin_amdgcn_fdot2(h2{whi[0], whi[1]}, ones, bsum, false);
         bsum = __builtin_amdgcn_fdot2(h2{whi[2], whi[3]}, ones, bsum, false);
@@ -332,17 +314,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
             const uint32_t src01[4] = {t01l, t01l, t01h, t01h};
             const uint32_t src23[4] = {t23l, t23l, t23h, t23h};
 #pragma unroll
-            for (int d = 0; d < 4; d++) {
-                const uint32_t sel = (d & 1) ? 0x04030402u : 0x04010400u;
-                const u32x2 bv = {__builtin_amdgcn_perm(kExp64, src01[d], sel), __builtin_amdgcn_perm(kExp64, src23[d], sel)};
+            for (int dd = 0; dd < 4; dd++) {
+                const uint32_t sel = (dd & 1) ? 0x04030402u : 0x04010400u;
+                const u32x2 bv = {__builtin_amdgcn_perm(kExp64, src01[dd], sel), __builtin_amdgcn_perm(kExp64, src23[dd], sel)};
                 const f16x4 bop = __builtin_bit_cast(f16x4, bv);
-                const int tt = 4 * hf + d;
+                const int tt = 4 * hf + dd;
                 oacc[tt] = mfma16(whi, bop, oacc[tt]);
                 oacc[tt] = mfma16(wlo, bop, oacc[tt]);
             }
         }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_wave_barrier();
     };
 
     // Loads are unconditional (an index past the end re-reads the last batch,
@@ -352,19 +332,21 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         while (true) {
             load(Bb, min(b + 1, last_b));
             __builtin_amdgcn_sched_barrier(0);
-            consume(A, b);
-            if (++b >= n_batches) break;
+            if (b == last_b) { consume(A, b, true); break; }
+            consume(A, b, false);
+            ++b;
             load(A, min(b + 1, last_b));
             __builtin_amdgcn_sched_barrier(0);
-            consume(Bb, b);
-            if (++b >= n_batches) break;
+            if (b == last_b) { consume(Bb, b, true); break; }
+            consume(Bb, b, false);
+            ++b;
         }
     }
 
-    // ---- per-wave totals: l over the 8 row slots; O of head lg, dims 8 lr .. +8
-    // minus the 1152 bias of V (the column sum of W over all rows) ----------------
-#pragma unroll
-    for (int h = 0; h < kGroup; h++) lsum[h] = sum_slots(lsum[h]);
+    // ---- per-wave totals: l and the W column sums over the 4 row groups; O of
+    // head lg, dims 8 lr .. +8 minus the 1152 bias of V -----------------------
+    lsum += swz_xor16(lsum);
+    lsum += __shfl_xor(lsum, 32);
     float bs = bsum + swz_xor16(bsum);
     bs += __shfl_xor(bs, 32);
     const float bias = 1152.0f * __shfl(bs, 4 * lg + (lr >> 2));
@@ -376,9 +358,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         *reinterpret_cast<float4*>(dst) = make_float4(ov[0], ov[1], ov[2], ov[3]);
         *reinterpret_cast<float4*>(dst + 4) = make_float4(ov[4], ov[5], ov[6], ov[7]);
     }
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < kGroup; h++) { ml_sh[wave][h][0] = m_run[h]; ml_sh[wave][h][1] = lsum[h]; }
+    if (lg == 0 && bq == 0) {   // lane 4 h: head h's (m, l), m in log2 units
+        ml_sh[wave][hq][0] = m_run * c2;
+        ml_sh[wave][hq][1] = lsum;
     }
     __syncthreads();
 

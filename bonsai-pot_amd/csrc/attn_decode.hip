@@ -51,11 +51,19 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+// Split-pass layouts, by KV heads per workgroup (kH):
+//  kH = 1: 4 waves, all on one KV head, each streaming every 4th 16-row batch;
+//  kH = 4: 8 waves, wave w on KV head 4 hg + (w & 3) and row set w >> 2, so the
+//          4 heads read the same rows together (512 contiguous bytes per row).
+template <int kH> struct SplitShape {
+    static constexpr int kWaves = kH == 1 ? 4 : 8;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kRowSets = kWaves / kH;
+    static constexpr int kWgPerCu = 8 / kWaves;   // at 2 waves per SIMD
+};
 constexpr int kRounds = 2;                 // rounds (8 rows each) per wave batch
 constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, pad (16-byte aligned rows)
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 128;          // the merge pass holds (m, l) of splits lane, lane + 64
 constexpr uint32_t kExp64 = 0x64646464u;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -113,11 +121,13 @@ __device__ __forceinline__ float sum_slots(float v) {
     return v;
 }
 
-template <bool kFused>
-__global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a) {
+template <bool kFused, int kH>
+__global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu) void decode_split_kernel(DecodeArgs a) {
+    constexpr int kWaves = SplitShape<kH>::kWaves, kRowSets = SplitShape<kH>::kRowSets;
+    constexpr int kQPerWave = kH * kGroup / kWaves;   // query heads normalized per wave (fused)
     __shared__ __attribute__((aligned(16))) float o_red[kWaves][kGroup][kHeadDim + 4];   // per-wave O
     __shared__ float ml_sh[kWaves][kGroup][2];
-    __shared__ __attribute__((aligned(16))) uint16_t qn_sh[kGroup][kHeadDim];
+    __shared__ __attribute__((aligned(16))) uint16_t qn_sh[kH][kGroup][kHeadDim];
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -128,14 +138,17 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     //        D lane holds O^T rows (head lg, block j) at dims (tile, lr).
     const int lr = lane & 15, lg = lane >> 4;
     const int hq = lr >> 2, bq = lr & 3;   // the (head, block) column of this lane
+    // Wave w streams KV head kH hg + (w % kH), row set w / kH (see SplitShape).
     // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
-    // linear id, so ids are laid out as [split / 8][g][split % 8] — the KV
-    // heads of one split share an XCD and hence its L2 copy of the rows' FP32
+    // linear id, so ids are laid out as [split / 8][hg][split % 8] — the head
+    // groups of one split share an XCD and hence its L2 copy of the rows' FP32
     // scale lines (one 128-byte line holds the scales of all heads of a row).
-    const uint32_t nkv = gridDim.x / ((a.n_splits + 7) / 8 * 8);
-    const uint32_t within = blockIdx.x % (8 * nkv);
-    const uint32_t g = within / 8;
-    const uint32_t split = blockIdx.x / (8 * nkv) * 8 + within % 8;
+    const int hw = wave % kH, rs = wave / kH;
+    const uint32_t ngr = gridDim.x / ((a.n_splits + 7) / 8 * 8);
+    const uint32_t within = blockIdx.x % (8 * ngr);
+    const uint32_t hg = within / 8;
+    const uint32_t g = hg * kH + hw;
+    const uint32_t split = blockIdx.x / (8 * ngr) * 8 + within % 8;
     if (split >= a.n_splits) return;
     const uint32_t row0 = min(split * a.split_len, a.n_rows);
     const uint32_t row_end = min(row0 + a.split_len, a.n_rows);
@@ -148,7 +161,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     const uint32_t vcol = g * kHeadDim + 8 * lr;           // p.v: dims 8 lr .. +8
     const uint32_t dcol = g * (kHeadDim / kBlock) + bq;    // scale of block bq
     auto load = [&](Batch& B, uint32_t b) {
-        const uint32_t r0 = row0 + 64u * b + 16u * wave;
+        const uint32_t r0 = row0 + 16u * (kRowSets * b + rs);
         const uint32_t rk = min(r0 + lr, row_end - 1);
         B.kq[0] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol));
         B.kq[1] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol + 16));
@@ -161,21 +174,31 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         }
     };
     const uint32_t n_rows = row_end - row0;
-    const uint32_t n_batches = n_rows > 16u * wave ? (n_rows - 16u * wave + 63u) / 64u : 0u;
+    const uint32_t n_batches =
+        n_rows > 16u * rs ? (n_rows - 16u * rs + 16u * kRowSets - 1) / (16u * kRowSets) : 0u;
     // ---- query-side loads first (unconditional): waiting for them below then
     // leaves the first batch of rows in flight (loads retire in order). -----------
     const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos) * kHeadDim + 2 * lane;
-    float qx0 = 0.f, qx1 = 0.f, w0 = 0.f, w1 = 0.f, c0 = 0.f, s0 = 0.f, x0 = 0.f, x1 = 0.f, kw0 = 0.f, kw1 = 0.f;
+    float qx[kQPerWave][2] = {}, w0 = 0.f, w1 = 0.f, c0 = 0.f, s0 = 0.f;
+    float x0 = 0.f, x1 = 0.f, kw0 = 0.f, kw1 = 0.f;
     Q16 qraw[4];   // q of head hq, dims 32 lg + 8 i .. +8
+    // Fused step: wave w normalizes the workgroup's query heads kQPerWave w ..,
+    // and waves w < 2 kH write row `pos` of KV head kH hg + (w % kH): K for
+    // w < kH, V otherwise.
+    const uint32_t qh0 = hg * kH * kGroup + kQPerWave * wave;
+    const uint32_t g_wb = hg * kH + wave % kH;
     if constexpr (kFused) {
-        const uint16_t* qr = a.q + static_cast<uint64_t>(g * kGroup + wave) * kHeadDim;
-        qx0 = h2f(qr[lane]);
-        qx1 = h2f(qr[lane + 64]);
+        const uint16_t* qr = a.q + static_cast<uint64_t>(qh0) * kHeadDim;
+#pragma unroll
+        for (int i = 0; i < kQPerWave; i++) {
+            qx[i][0] = h2f(qr[i * kHeadDim + lane]);
+            qx[i][1] = h2f(qr[i * kHeadDim + lane + 64]);
+        }
         w0 = h2f(a.w_norms[a.w_q_off + lane]);
         w1 = h2f(a.w_norms[a.w_q_off + lane + 64]);
         c0 = h2f(cs[0]);
         s0 = h2f(cs[1]);
-        const uint16_t* src = ((wave & 1) == 0 ? a.k_cur : a.v_cur) + g * kHeadDim;   // writeback input
+        const uint16_t* src = (wave < kH ? a.k_cur : a.v_cur) + g_wb * kHeadDim;   // writeback input
         x0 = h2f(src[lane]);
         x1 = h2f(src[lane + 64]);
         kw0 = h2f(a.w_norms[a.w_k_off + lane]);
@@ -192,22 +215,26 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (kFused) {
-        // q_norm_rope for head 4g + wave (q_norm_rope_fused.wgsl:38-96), into LDS.
-        const uint32_t h = g * kGroup + wave;
-        float o0, o1;
-        norm_rope_pair(qx0, qx1, w0, w1, c0, s0, a.eps, o0, o1);
-        qn_sh[wave][lane] = f2h(o0);
-        qn_sh[wave][lane + 64] = f2h(o1);
-        if (split == 0) {
-            a.q_norm[h * kHeadDim + lane] = f2h(o0);
-            a.q_norm[h * kHeadDim + lane + 64] = f2h(o1);
+        // q_norm_rope (q_norm_rope_fused.wgsl:38-96), into LDS.
+        uint16_t* qn = &qn_sh[0][0][0] + kQPerWave * wave * kHeadDim;
+        uint16_t* qg = a.q_norm + static_cast<uint64_t>(qh0) * kHeadDim;
+#pragma unroll
+        for (int i = 0; i < kQPerWave; i++) {
+            float o0, o1;
+            norm_rope_pair(qx[i][0], qx[i][1], w0, w1, c0, s0, a.eps, o0, o1);
+            qn[i * kHeadDim + lane] = f2h(o0);
+            qn[i * kHeadDim + lane + 64] = f2h(o1);
+            if (split == 0) {
+                qg[i * kHeadDim + lane] = f2h(o0);
+                qg[i * kHeadDim + lane + 64] = f2h(o1);
+            }
         }
-        if (split == a.n_splits - 1 && wave < 2) {
-            // kv_writeback of row `pos` for KV head g (kv_writeback_fused.wgsl):
-            // wave 0 writes K (norm + RoPE + Q8_0), wave 1 writes V (Q8_0).
-            const uint64_t d_idx = static_cast<uint64_t>(a.pos) * nb_row + g * (kHeadDim / kBlock);
-            const uint64_t qs_idx = static_cast<uint64_t>(a.pos) * kv_dim + g * kHeadDim;
-            if (wave == 0) {
+        if (split == a.n_splits - 1 && wave < 2 * kH) {
+            // kv_writeback of row `pos` for KV head g_wb (kv_writeback_fused.wgsl):
+            // K (norm + RoPE + Q8_0) or V (Q8_0).
+            const uint64_t d_idx = static_cast<uint64_t>(a.pos) * nb_row + g_wb * (kHeadDim / kBlock);
+            const uint64_t qs_idx = static_cast<uint64_t>(a.pos) * kv_dim + g_wb * kHeadDim;
+            if (wave < kH) {
                 norm_rope_pair(x0, x1, kw0, kw1, c0, s0, a.eps, x0, x1);
                 quantize_store_pair(x0, x1, lane, const_cast<float*>(a.k.d) + d_idx,
                                     const_cast<int8_t*>(a.k.qs) + qs_idx);
@@ -218,7 +245,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
         }
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; i++) qraw[i] = *reinterpret_cast<const Q16*>(&qn_sh[hq][32 * lg + 8 * i]);
+        for (int i = 0; i < 4; i++) qraw[i] = *reinterpret_cast<const Q16*>(&qn_sh[hw][hq][32 * lg + 8 * i]);
     }
     // ---- B operand of q.k: q of head hq on block bq's k slots, zero elsewhere;
     // and the bias 1152 * sum(q over block bq) of the exact-f16 K trick. -----------
@@ -261,7 +288,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
             s[j] = v;
         }
         if (tail) {
-            const uint32_t r0 = row0 + 64u * b + 16u * wave + 4u * lg;
+            const uint32_t r0 = row0 + 16u * (kRowSets * b + rs) + 4u * lg;
 #pragma unroll
             for (int j = 0; j < 4; j++) s[j] = r0 + j < row_end ? s[j] : -INFINITY;
         }
@@ -364,31 +391,38 @@ __global__ __launch_bounds__(kThreads, 2) void decode_split_kernel(DecodeArgs a)
     }
     __syncthreads();
 
-    // ---- merge the 4 waves; thread t -> head t>>6, dims 2*(t&63), +1 -----------
-    const int fh = t >> 6, fd = 2 * (t & 63);
+    // ---- merge the row sets: thread t -> query head t / (128 / kE) of the
+    // workgroup's 4 kH (KV head fw, its head fh), dims kE (t % (128 / kE)) .. ----
+    constexpr int kE = kH * kGroup * kHeadDim / (64 * kWaves);   // 2 or 4 dims per thread
+    constexpr int kTpH = kHeadDim / kE;                           // threads per query head
+    const int fq = t / kTpH, fw = fq >> 2, fh = fq & 3, fd = kE * (t % kTpH);
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, ml_sh[w][fh][0]);
-    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int r = 0; r < kRowSets; r++) M = fmaxf(M, ml_sh[fw + kH * r][fh][0]);
+    float L = 0.0f;
+    float o[kE] = {};
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) {
+    for (int r = 0; r < kRowSets; r++) {
+        const int w = fw + kH * r;
         const float mw = ml_sh[w][fh][0];
-        const float e = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);   // waves without rows
+        const float e = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);   // row sets without rows
         L = __builtin_fmaf(e, ml_sh[w][fh][1], L);
-        const float2 v = *reinterpret_cast<const float2*>(&o_red[w][fh][fd]);
-        o0 = __builtin_fmaf(e, v.x, o0);
-        o1 = __builtin_fmaf(e, v.y, o1);
+#pragma unroll
+        for (int k = 0; k < kE; k++) o[k] = __builtin_fmaf(e, o_red[w][fh][fd + k], o[k]);
     }
-    const uint32_t qhd = g * kGroup + fh;
+    const uint32_t qhd = (hg * kH + fw) * kGroup + fh;
     if (!kFused && a.n_splits == 1) {
         const float inv_l = 1.0f / L;
-        uint32_t* out = reinterpret_cast<uint32_t*>(a.out + static_cast<uint64_t>(qhd) * kHeadDim + fd);
-        *out = static_cast<uint32_t>(f2h(o0 * inv_l)) | (static_cast<uint32_t>(f2h(o1 * inv_l)) << 16);
+#pragma unroll
+        for (int k = 0; k < kE; k += 2)
+            *reinterpret_cast<uint32_t*>(a.out + static_cast<uint64_t>(qhd) * kHeadDim + fd + k) =
+                static_cast<uint32_t>(f2h(o[k] * inv_l)) | (static_cast<uint32_t>(f2h(o[k + 1] * inv_l)) << 16);
         return;
     }
     float* part = a.partials + (static_cast<uint64_t>(qhd) * a.n_splits + split) * kPartStride;
-    *reinterpret_cast<float2*>(part + fd) = make_float2(o0, o1);
-    if ((t & 63) == 0) *reinterpret_cast<float2*>(part + kHeadDim) = make_float2(M, L);
+#pragma unroll
+    for (int k = 0; k < kE; k += 2) *reinterpret_cast<float2*>(part + fd + k) = make_float2(o[k], o[k + 1]);
+    if (t % kTpH == 0) *reinterpret_cast<float2*>(part + kHeadDim) = make_float2(M, L);
 }
 
 // One wave per (query head, 32-dim chunk).
@@ -409,9 +443,12 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
         const uint32_t s = min(static_cast<uint32_t>((lane >> 3) + 8 * i), ns - 1);
         ov[i] = *reinterpret_cast<const float4*>(ph + static_cast<uint64_t>(s) * kPartStride + 32 * c + 4 * f4);
     }
-    const uint32_t ls = min(static_cast<uint32_t>(lane), ns - 1);
-    const float2 ml = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls) * kPartStride + kHeadDim);
-    const float m_s = static_cast<uint32_t>(lane) < ns ? ml.x : -INFINITY;
+    // (m, l) of splits lane and lane + 64.
+    const uint32_t ls0 = min(static_cast<uint32_t>(lane), ns - 1), ls1 = min(static_cast<uint32_t>(lane) + 64u, ns - 1);
+    const float2 ml0 = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls0) * kPartStride + kHeadDim);
+    const float2 ml1 = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls1) * kPartStride + kHeadDim);
+    const float m_s0 = static_cast<uint32_t>(lane) < ns ? ml0.x : -INFINITY;
+    const float m_s1 = static_cast<uint32_t>(lane) + 64u < ns ? ml1.x : -INFINITY;
 
     float s_new = -INFINITY;   // log2-domain score of the new row (fused step)
     // Row `pos` of V for dims d0 .. d0 + 3 (lanes 0-7 use it), loaded up front with
@@ -436,15 +473,16 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
         const uint16_t qv = static_cast<uint16_t>(__shfl(static_cast<int>(c < 2 ? qa : qb), static_cast<int>((32 * c + lane) & 63)));
         if (lane < 32) a.q_act[h * kHeadDim + 32 * c + lane] = qv;
     }
-    const float M = fmaxf(wave_max(m_s), s_new);
-    const float w = m_s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s - M);
+    const float M = fmaxf(wave_max(fmaxf(m_s0, m_s1)), s_new);
+    const float w0 = m_s0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s0 - M);   // 0 for splits >= ns
+    const float w1 = m_s1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s1 - M);
     const float w_new = kFused ? __builtin_amdgcn_exp2f(s_new - M) : 0.0f;
-    const float L = wave_sum(w * (static_cast<uint32_t>(lane) < ns ? ml.y : 0.0f)) + w_new;
+    const float L = wave_sum(w0 * (m_s0 == -INFINITY ? 0.0f : ml0.y) + w1 * (m_s1 == -INFINITY ? 0.0f : ml1.y)) + w_new;
 
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < kMaxSplits / 8; i++) {
-        const float wi = __shfl(w, (lane >> 3) + 8 * i);   // 0 for splits >= ns
+        const float wi = __shfl(i < 8 ? w0 : w1, (lane >> 3) + 8 * (i & 7));
         acc.x = __builtin_fmaf(wi, ov[i].x, acc.x);
         acc.y = __builtin_fmaf(wi, ov[i].y, acc.y);
         acc.z = __builtin_fmaf(wi, ov[i].z, acc.z);
@@ -473,37 +511,52 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
 }  // namespace
 
 void decode_plan(uint32_t n_rows, uint32_t n_kv_head, int cu_count, uint32_t min_split_rows,
-                 uint32_t* split_len, uint32_t* n_splits) {
-    // Enough workgroups to cover the CUs twice, but at least min_split_rows
-    // rows each (fewer partials at short context) and at most kMaxSplits
-    // splits; rows per split are a multiple of 64 (one batch of all 4 waves).
-    const uint32_t target = static_cast<uint32_t>(cu_count > 0 ? cu_count : 256) * 2;
-    uint32_t want = (target + n_kv_head - 1) / n_kv_head;
+                 uint32_t wide_min_rows, uint32_t* split_len, uint32_t* n_splits, uint32_t* heads_per_wg) {
+    // Layout: 4 KV heads per workgroup from wide_min_rows rows on (long
+    // contexts: rows are read whole), else 1 (short contexts: 4 waves per head
+    // keep each wave's chain short). Then enough workgroups to fill every CU
+    // at 2 waves per SIMD, but at least min_split_rows rows each (fewer
+    // partials at short context) and at most kMaxSplits splits; rows per split
+    // are a multiple of one batch of all row sets.
+    const uint32_t h = n_rows >= wide_min_rows && n_kv_head % 4 == 0 ? 4 : 1;
+    const uint32_t wg_per_cu = h == 1 ? SplitShape<1>::kWgPerCu : SplitShape<4>::kWgPerCu;
+    const uint32_t batch_rows = 16u * (h == 1 ? SplitShape<1>::kRowSets : SplitShape<4>::kRowSets);
+    const uint32_t target = static_cast<uint32_t>(cu_count > 0 ? cu_count : 256) * wg_per_cu;
+    const uint32_t groups = n_kv_head / h;
+    uint32_t want = (target + groups - 1) / groups;
     if (want < 1) want = 1;
     if (want > kMaxSplits) want = kMaxSplits;
     uint32_t len = (n_rows + want - 1) / want;
     if (len < min_split_rows) len = min_split_rows;
-    len = (len + 63) / 64 * 64;
+    len = (len + batch_rows - 1) / batch_rows * batch_rows;
     *split_len = len;
     *n_splits = n_rows == 0 ? 1 : (n_rows + len - 1) / len;
+    *heads_per_wg = h;
 }
 
 uint32_t decode_max_splits() { return kMaxSplits; }
 uint32_t decode_partial_stride() { return kPartStride; }
 
-static dim3 split_grid(const DecodeArgs& a, uint32_t n_kv_head) {
-    return dim3((a.n_splits + 7) / 8 * 8 * n_kv_head);
+template <bool kFused>
+static void launch_split(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
+    const uint32_t rows8 = (a.n_splits + 7) / 8 * 8;
+    if (a.heads_per_wg == 4)
+        hipLaunchKernelGGL((decode_split_kernel<kFused, 4>), dim3(rows8 * (n_kv_head / 4)),
+                           dim3(SplitShape<4>::kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<kFused, 1>), dim3(rows8 * n_kv_head),
+                           dim3(SplitShape<1>::kThreads), 0, s, a);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(decode_split_kernel<false>, split_grid(a, n_kv_head), dim3(kThreads), 0, s, a);
+    launch_split<false>(a, n_kv_head, s);
     if (a.n_splits > 1)
         hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_decode_step(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(decode_split_kernel<true>, split_grid(a, n_kv_head), dim3(kThreads), 0, s, a);
+    launch_split<true>(a, n_kv_head, s);
     hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
     return hipGetLastError();
 }

@@ -40,6 +40,7 @@ struct bp_model {
     uint64_t partials_floats;
     uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
     uint32_t decode_min_split_rows;
+    uint32_t decode_wide_min_rows;
     bool lost;
     std::string lost_message;
 };
@@ -149,8 +150,8 @@ bp::DecodeArgs decode_args(const bp_model* m, void* act, uint32_t q_off, uint32_
     a.partials = m->partials;
     a.kv_dim = m->kv_dim;
     a.n_rows = n_rows;
-    bp::decode_plan(n_rows, m->cfg.n_kv_head, m->cu_count, m->decode_min_split_rows, &a.split_len,
-                    &a.n_splits);
+    bp::decode_plan(n_rows, m->cfg.n_kv_head, m->cu_count, m->decode_min_split_rows,
+                    m->decode_wide_min_rows, &a.split_len, &a.n_splits, &a.heads_per_wg);
     a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:838
     return a;
 }
@@ -240,6 +241,12 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
     if (const char* env = std::getenv("BP_DECODE_MIN_SPLIT_ROWS")) {
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 32 && v <= (1 << 20)) m->decode_min_split_rows = static_cast<uint32_t>(v);
+    }
+    // Rows from which the split pass reads 4 KV heads per workgroup.
+    m->decode_wide_min_rows = 8192;
+    if (const char* env = std::getenv("BP_DECODE_WIDE_MIN_ROWS")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 0) m->decode_wide_min_rows = static_cast<uint32_t>(v);
     }
     m->partials_floats = static_cast<uint64_t>(cfg->n_head) * bp::decode_max_splits() *
                          bp::decode_partial_stride();

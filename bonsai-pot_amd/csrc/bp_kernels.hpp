@@ -55,6 +55,7 @@ struct DecodeArgs {
     uint32_t n_rows;          // rows streamed by the split pass: [0, n_rows)
     uint32_t split_len;       // rows per workgroup, multiple of 32
     uint32_t n_splits;        // >= 1
+    uint32_t heads_per_wg;    // split-pass layout: 1 or 4 KV heads per workgroup
     float scale;
     // Fused decode step only (q_norm_rope + kv_writeback of row `pos` + attention
     // over rows [0, pos]): the split pass normalizes q itself and writes cache row
@@ -87,9 +88,10 @@ hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t 
                               hipStream_t s);
 hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uint32_t m_tokens,
                                hipStream_t s);
-// Split-K plan of a decode over n_rows rows (1 <= n_splits <= decode_max_splits()).
+// Split-K plan of a decode over n_rows rows (1 <= n_splits <= decode_max_splits())
+// and the split pass's layout (heads_per_wg = 4 from wide_min_rows rows on).
 void decode_plan(uint32_t n_rows, uint32_t n_kv_head, int cu_count, uint32_t min_split_rows,
-                 uint32_t* split_len, uint32_t* n_splits);
+                 uint32_t wide_min_rows, uint32_t* split_len, uint32_t* n_splits, uint32_t* heads_per_wg);
 uint32_t decode_max_splits();
 uint32_t decode_partial_stride();   // floats per (head, split) partial
 // Plain decode (q already normalized, cache row already written): one launch

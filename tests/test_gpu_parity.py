@@ -68,9 +68,16 @@ def test_writeback_special_values(cuda):
     assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v)
 
 
+# The split pass has two layouts (1 or 4 KV heads per workgroup), chosen by
+# context length; BP_DECODE_WIDE_MIN_ROWS forces either one at model creation.
+LAYOUTS = {"narrow": str(2**31), "wide": "0"}
+
+
+@pytest.mark.parametrize("layout_name", sorted(LAYOUTS))
 @pytest.mark.parametrize("pos", [0, 1, 31, 512, 4096])
-def test_decode_vs_oracle(cuda, pos):
-    _say(f"[decode] pos={pos}")
+def test_decode_vs_oracle(cuda, monkeypatch, pos, layout_name):
+    monkeypatch.setenv("BP_DECODE_WIDE_MIN_ROWS", LAYOUTS[layout_name])
+    _say(f"[decode] pos={pos} layout={layout_name}")
     cfg = layout.Config(n_layer=2)
     sc = Scenario(cfg, max_seq=pos + 8, m_tokens=1, seed=100 + pos)
     _prefill_cache(sc, 1, pos, seed=200 + pos)
@@ -184,11 +191,13 @@ def test_decode_repeated_calls_fresh_partials(cuda):
         assert_attn_close(dev.out_f32(1)[0], want, f"repeat step {step} layer {il} pos {pos}")
 
 
+@pytest.mark.parametrize("layout_name", sorted(LAYOUTS))
 @pytest.mark.parametrize("pos,w_std", [(0, 0.0), (1, 0.1), (40, 0.1), (4096, 0.0), (32768, 0.1)])
-def test_fused_decode_step(cuda, pos, w_std):
+def test_fused_decode_step(cuda, monkeypatch, pos, w_std, layout_name):
     """bp_dispatch_attention_decode_step == q_norm_rope + kv_writeback + decode:
     normalized q and cache bytes bit-exact, attention output within tolerance."""
-    _say(f"[decode-step] pos={pos}")
+    monkeypatch.setenv("BP_DECODE_WIDE_MIN_ROWS", LAYOUTS[layout_name])
+    _say(f"[decode-step] pos={pos} layout={layout_name}")
     cfg = layout.Config(n_layer=2)
     sc = Scenario(cfg, max_seq=pos + 4, m_tokens=1, seed=700 + pos, w_std=w_std)
     _prefill_cache(sc, 1, pos, seed=800 + pos)

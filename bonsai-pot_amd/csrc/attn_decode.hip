@@ -4,29 +4,31 @@
 // (reference repository): scores s_t = (q . k_t) / sqrt(128) over the cache
 // rows, softmax in f32, o = sum p_t v_t, f16 output. Two passes:
 //
-// Split pass (decode_split_kernel) — one 256-thread workgroup per (KV head,
-// range of `split_len` rows), the 1-D grid ordered XCD-aware:
-//  * Each wave streams its own rows with no workgroup barrier in the main
-//    loop: a wave "round" is 8 rows, lane (slot = lane>>3, seg = lane&7)
-//    reading the 16 contiguous qs bytes of dims [16 seg, 16 seg + 16) of its
-//    row plus that block's FP32 scale — eight full 128-byte row segments per
-//    load instruction. Waves interleave rounds (wave w takes rounds w, w+4,..)
-//    and the next batch of kRounds rounds is loaded before the current one is
-//    consumed (register double buffering). Loads are never predicated: rows
-//    past the range are clamped onto its last row and masked by their score.
-//  * q.k runs on v_dot2_f32_f16: q is f16 already, and each K byte pair
-//    becomes an exact f16 pair with one v_perm_b32 — byte (k xor 0x80) under
-//    exponent byte 0x64 is the f16 value 1152 + k — so
-//      q.k = dot2(q, 1152 + k) - 1152 * sum(q).
-//    p.v stays in f32 FMAs (unsigned-byte converts, the same +128 bias
-//    removed algebraically) so the softmax weights are never rounded to f16.
-//  * Online softmax in the exp2 domain; the batch max is shared by the whole
-//    wave, so running sums need no cross-lane reduction until the end and O
-//    is rescaled only when some max moved. Lane reductions use DPP / swizzle.
-//  * O is summed over row-slot pairs with one DPP add and handed to LDS, where
-//    the 4 waves x 4 slot pairs are merged (log-sum-exp over the waves) into one
-//    partial (o[128], m, l) per query head, written with plain stores; with a
-//    single split the output is written directly and the merge pass is skipped.
+// Split pass (decode_split_kernel) — one workgroup per (group of KV heads,
+// range of `split_len` rows), the 1-D grid ordered XCD-aware. Each wave owns
+// one KV head (its 4 query heads) and streams 16-row batches with no
+// workgroup barrier in the main loop, the next batch loaded before the
+// current one is consumed (register double buffering). Loads are never
+// predicated: rows past the range are clamped onto its last row and masked
+// by their score. Two layouts (SplitShape): 4 waves on one KV head at short
+// context; 4 KV heads x 2 row sets per 8-wave workgroup at long context, so
+// that the heads of a row are read together.
+//  * Both products run on the matrix core in f16 with f32 accumulation, on
+//    exact f16 images of the int8 values: byte (x xor 0x80) under exponent
+//    byte 0x64 is the f16 value 1152 + x (one v_perm_b32 per byte pair), and
+//    the 1152 bias is removed algebraically.
+//  * q.k (16x16x32): A = the batch's K rows (m = row), B = q of the 4 heads
+//    with the k-slots of each Q8_0 block routed to its own column (h, b), so
+//    D holds per-block partial dots and the FP32 block scales are applied
+//    after the MFMA: s = sum_b d_b (D_b - 1152 sum_b q).
+//  * Online softmax in the exp2 domain, per lane (row group, head); O is
+//    rescaled only when some max moved (a wave ballot).
+//  * p.v (16x16x16): O^T = W^T V with W = p d_v, split into two f16 terms
+//    (hi + lo, so the weights keep f32-like precision), V bytes transposed
+//    into the B layout with v_perm_b32.
+//  * The row sets of a KV head are merged through LDS (log-sum-exp) into one
+//    partial (o[128], m, l) per query head; with a single split the output is
+//    written directly and the merge pass is skipped.
 //
 // Merge pass (decode_merge_kernel) — one 64-lane workgroup per (query head,
 // 32-dim chunk): log-sum-exp over the splits (attention_merge.wgsl:85-129),
@@ -61,7 +63,6 @@ template <int kH> struct SplitShape {
     static constexpr int kRowSets = kWaves / kH;
     static constexpr int kWgPerCu = 8 / kWaves;   // at 2 waves per SIMD
 };
-constexpr int kRounds = 2;                 // rounds (8 rows each) per wave batch
 constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, pad (16-byte aligned rows)
 constexpr int kMaxSplits = 128;          // the merge pass holds (m, l) of splits lane, lane + 64
 constexpr uint32_t kExp64 = 0x64646464u;
@@ -86,13 +87,7 @@ __device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
 __device__ __forceinline__ float pick4(f32x4 v, int i) {
     return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
 }
-__device__ __forceinline__ float pick4(const float (&v)[4], int i) {
-    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
-}
 
-__device__ __forceinline__ float ub(uint32_t w, int i) {   // v_cvt_f32_ubyte{i}
-    return static_cast<float>((w >> (8 * i)) & 0xffu);
-}
 template <int kCtrl>
 __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
@@ -100,20 +95,7 @@ __device__ __forceinline__ float dpp_f(float v) {
 __device__ __forceinline__ float swz_xor16(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
-// Sum over the 8 lanes of a row slot (lanes 8k..8k+7).
-__device__ __forceinline__ float sum8(float v) {
-    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
-    v += dpp_f<0x141>(v);   // row_half_mirror
-    return v;
-}
-// Max / sum over lanes l, l^8, l^16, l^32 (the 8 row slots, same seg).
-__device__ __forceinline__ float max_slots(float v) {
-    v = fmaxf(v, dpp_f<0x128>(v));   // row_ror:8 == xor 8 within 16 lanes
-    v = fmaxf(v, swz_xor16(v));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
-}
+// Sum over lanes l, l^8, l^16, l^32.
 __device__ __forceinline__ float sum_slots(float v) {
     v += dpp_f<0x128>(v);
     v += swz_xor16(v);

@@ -100,6 +100,86 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return static_cast<uint32_t>(f2h(a)) | (static_cast<uint32_t>(f2h(b)) << 16);
 }
 
+// Dequantization pass: one 256-thread workgroup per (64-row chunk, KV head)
+// writes the chunk's f16 K rows and its V^T (dims x slots, keys in v_slot
+// order) to the image, zeros past n_rows. Values are f16(d * q), computed as
+// in the decode path: byte (q xor 0x80) under exponent byte 0x64 is the exact
+// f16 value 1152 + q, and fma(1152 + q, d, -1152 d) is rounded to f16 once.
+//  K: thread t -> row t >> 2, Q8_0 block t & 3 (32 dims, 64 bytes out).
+//  V: thread t -> rows 4 (t >> 4) .. +3, dims 8 (t & 15) .. +7; each dim's 4
+//     values are 4 consecutive V^T slots, one 8-byte LDS write.
+__global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
+    const int t = threadIdx.x;
+    const uint32_t c = blockIdx.x, g = blockIdx.y;
+    const uint32_t nb_row = a.kv_dim / kBlock;
+    const uint32_t last = a.n_rows - 1;
+    // ---- loads (unconditional, clamped rows; rows past n_rows get d = 0) ----
+    const int kr = t >> 2, kb = t & 3;
+    const uint32_t krow = c * kChunk + kr, krc = min(krow, last);
+    const uint8_t* kqp = reinterpret_cast<const uint8_t*>(a.k.qs) + static_cast<uint64_t>(krc) * a.kv_dim + g * kHeadDim + 32 * kb;
+    const U4 kq0 = *reinterpret_cast<const U4*>(kqp), kq1 = *reinterpret_cast<const U4*>(kqp + 16);
+    float kd = a.k.d[static_cast<uint64_t>(krc) * nb_row + g * (kHeadDim / kBlock) + kb];
+    const int vq4 = t >> 4, vdg = t & 15;
+    uint2 vq[4];
+    float vd[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = c * kChunk + 4 * vq4 + i, rc = min(row, last);
+        vq[i] = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.v.qs) +
+                                                static_cast<uint64_t>(rc) * a.kv_dim + g * kHeadDim + 8 * vdg);
+        vd[i] = a.v.d[static_cast<uint64_t>(rc) * nb_row + g * (kHeadDim / kBlock) + (vdg >> 2)];
+        if (row > last) vd[i] = 0.0f;
+    }
+    if (krow > last) kd = 0.0f;
+    auto deq = [](uint32_t x, uint32_t sel, float d, float cc) {   // x already xor 0x80808080
+        const f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, sel));
+        const f16x2 r = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.x), d, cc)),
+                         static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.y), d, cc))};
+        return __builtin_bit_cast(uint32_t, r);
+    };
+    // ---- K rows ----
+    {
+        const float kc = -1152.0f * kd;
+        uint32_t w[16];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t x = (i < 4 ? kq0.w[i] : kq1.w[i - 4]) ^ 0x80808080u;
+            w[2 * i] = deq(x, 0x04010400u, kd, kc);
+            w[2 * i + 1] = deq(x, 0x04030402u, kd, kc);
+        }
+        U4* kdst = reinterpret_cast<U4*>(a.k16 + ((static_cast<uint64_t>(g) * a.ws_chunks + c) * kChunk + kr) * kHeadDim + 32 * kb);
+#pragma unroll
+        for (int i = 0; i < 4; i++) kdst[i] = U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
+    }
+    // ---- V^T through LDS ----
+    {
+        float vc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) vc[i] = -1152.0f * vd[i];
+        const int slot = v_slot(4 * vq4);   // rows 4 vq4 .. +3 -> slots slot .. slot + 3
+#pragma unroll
+        for (int e = 0; e < 8; e++) {   // dim 8 vdg + e
+            uint16_t hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t word = (e < 4 ? vq[i].x : vq[i].y) ^ 0x80808080u;
+                const uint32_t sel = 0x04040400u | static_cast<uint32_t>(e & 3);
+                const _Float16 x = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, word, sel)).x;
+                hv[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__builtin_fmaf(static_cast<float>(x), vd[i], vc[i])));
+            }
+            *reinterpret_cast<uint2*>(&vt[8 * vdg + e][slot]) =
+                make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16), hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
+        }
+    }
+    __syncthreads();
+    // V^T rows: thread t -> dim t >> 1, slots 32 (t & 1) .. +32.
+    const int dim = t >> 1, s0 = 32 * (t & 1);
+    uint16_t* vdst = a.vt16 + ((static_cast<uint64_t>(g) * a.ws_chunks + c) * kHeadDim + dim) * kChunk + s0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) *reinterpret_cast<U4*>(vdst + 8 * i) = *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
+}
+
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // lds[stream][buf]: staged chunk (K rows then V^T rows), 2 streams x 2 buffers.
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
@@ -108,8 +188,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int lane = t & 63, wave = t >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const bool is_b = (wave & 4) != 0;               // B wave (heavy tile) or A wave
-    const uint32_t g = blockIdx.y;
-    const uint32_t tile_a = blockIdx.x, tile_b = a.n_tiles - 1 - blockIdx.x;   // tile_b >= tile_a
+    // 1-D grid, KV head fastest: workgroups are dealt to the 8 XCDs round-robin,
+    // so with 8 KV heads each XCD serves one head and its L2 holds that head's
+    // K/V for all the head's tile pairs.
+    const uint32_t nkv = a.kv_dim / kHeadDim;
+    const uint32_t g = blockIdx.x % nkv, pair = blockIdx.x / nkv;
+    const uint32_t tile_a = pair, tile_b = a.n_tiles - 1 - pair;   // tile_b >= tile_a
     const uint32_t h0 = g * kGroup + kHeadsPerWave * ((wave >> 1) & 1);        // first query head
     const uint32_t utok = 16 * (wave & 1);            // unit's first token within its tile
     const float c2 = a.scale * 1.4426950408889634f;   // scores in log2 units
@@ -178,73 +262,27 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // the second half of it); B waves on tile B.
     start_unit(is_b || n_a == 0 ? tile_b : tile_a);
 
-    // ---- staging ------------------------------------------------------------
-    // K: thread owns chunk row (t >> 3), dims [16 (t & 7), +16).
-    // V: thread owns chunk rows 2u, 2u+1 (u = t >> 4), dims [8 (t & 15), +8);
-    //    it writes each dim's two values as one 4-byte word of V^T (the rows
-    //    of a key pair are adjacent slots).
-    // Loads are unconditional from a clamped row (a predicated load becomes a
-    // branch that drains all outstanding loads); rows past kend_b are zeroed
-    // through their scale.
-    const int krow = t >> 3, kseg = t & 7;
-    const int vu = t >> 4, vdq = t & 15;
-    const uint64_t kv_dim = a.kv_dim;
-    const uint32_t nb_row = a.kv_dim / kBlock;
-    const uint32_t kcol = g * kHeadDim + 16 * kseg, kdcol = g * (kHeadDim / kBlock) + (kseg >> 1);
-    const uint32_t vcol = g * kHeadDim + 8 * vdq, vdcol = g * (kHeadDim / kBlock) + (vdq >> 2);
-    struct Stage { U4 kq; uint2 v0, v1; float kd, vd0, vd1; };
+    // ---- staging: copy a chunk's f16 K rows and V^T from the image -------------
+    // 32 KB per chunk = 4 16-byte pieces per thread: K piece p (= t, t + 512) is
+    // row p >> 4, dims 8 (p & 15) ..; V^T piece p is dim p >> 3, slots 8 (p & 7) ..
+    const uint16_t* k16 = a.k16 + static_cast<uint64_t>(g) * a.ws_chunks * kChunk * kHeadDim;
+    const uint16_t* vt16 = a.vt16 + static_cast<uint64_t>(g) * a.ws_chunks * kHeadDim * kChunk;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    struct Stage { u32x4 k0, k1, v0, v1; };   // vector members: kept in registers
     auto load_chunk = [&](Stage& S, uint32_t c) {
-        const uint32_t kr = c * kChunk + krow, vr = c * kChunk + 2 * vu;
-        const uint64_t krc = min(kr, kend_b - 1), vr0 = min(vr, kend_b - 1), vr1 = min(vr + 1, kend_b - 1);
-        S.kq = *reinterpret_cast<const U4*>(a.k.qs + krc * kv_dim + kcol);
-        S.v0 = *reinterpret_cast<const uint2*>(a.v.qs + vr0 * kv_dim + vcol);
-        S.v1 = *reinterpret_cast<const uint2*>(a.v.qs + vr1 * kv_dim + vcol);
-        S.kd = a.k.d[krc * nb_row + kdcol];
-        S.vd0 = a.v.d[vr0 * nb_row + vdcol];
-        S.vd1 = a.v.d[vr1 * nb_row + vdcol];
-        if (kr >= kend_b) S.kd = 0.0f;
-        if (vr >= kend_b) S.vd0 = 0.0f;
-        if (vr + 1 >= kend_b) S.vd1 = 0.0f;
-    };
-    // Dequantization d * q -> f16: byte (q xor 0x80) under exponent byte 0x64
-    // is the exact f16 value x = 1152 + q (one v_perm per two values), and
-    // fma(x, d, -1152 d) = d * q (up to the f32 rounding of 1152 d) is rounded
-    // to f16 once by the mixed-precision FMA.
-    auto deq_pair = [&](uint32_t x, uint32_t sel, float d, float c) {
-        const f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, sel));
-        const f16x2 r = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.x), d, c)),
-                         static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.y), d, c))};
-        return __builtin_bit_cast(uint32_t, r);
+        const u32x4* kc = reinterpret_cast<const u32x4*>(k16 + static_cast<uint64_t>(c) * kChunk * kHeadDim);
+        const u32x4* vc = reinterpret_cast<const u32x4*>(vt16 + static_cast<uint64_t>(c) * kHeadDim * kChunk);
+        S.k0 = kc[t];
+        S.k1 = kc[t + kThreads];
+        S.v0 = vc[t];
+        S.v1 = vc[t + kThreads];
     };
     auto store_chunk = [&](const Stage& S, uint16_t* buf) {
-        U4 lo, hi;
-        const float kc = -1152.0f * S.kd;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t x = S.kq.w[i] ^ 0x80808080u;   // dims 4i .. 4i+3 of the 16
-            const uint32_t p01 = deq_pair(x, 0x04010400u, S.kd, kc), p23 = deq_pair(x, 0x04030402u, S.kd, kc);
-            if (i < 2) { lo.w[2 * i] = p01; lo.w[2 * i + 1] = p23; }
-            else { hi.w[2 * i - 4] = p01; hi.w[2 * i - 3] = p23; }
-        }
-        uint16_t* kr = buf + krow * kKStride + 16 * kseg;
-        *reinterpret_cast<U4*>(kr) = lo;
-        *reinterpret_cast<U4*>(kr + 8) = hi;
-        uint16_t* vb = buf + kKHalves;
-        const int slot = v_slot(2 * vu);   // even; 2u + 1 sits in slot + 1
-        const float vc0 = -1152.0f * S.vd0, vc1 = -1152.0f * S.vd1;
-        const uint32_t w0[2] = {S.v0.x ^ 0x80808080u, S.v0.y ^ 0x80808080u};
-        const uint32_t w1[2] = {S.v1.x ^ 0x80808080u, S.v1.y ^ 0x80808080u};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int row = 8 * vdq + i;
-            // rows 2u, 2u+1 of dim row: interleave their bytes, then one pair each
-            const uint32_t sel = 0x04000400u | (static_cast<uint32_t>(i & 3) << 16) | static_cast<uint32_t>(i & 3);
-            const f16x2 a0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w0[i >> 2], sel));
-            const f16x2 a1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w1[i >> 2], sel));
-            const f16x2 r = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(a0.x), S.vd0, vc0)),
-                             static_cast<_Float16>(__builtin_fmaf(static_cast<float>(a1.x), S.vd1, vc1))};
-            *reinterpret_cast<uint32_t*>(vb + v_addr(row, slot)) = __builtin_bit_cast(uint32_t, r);
-        }
+        const int p0 = t, p1 = t + kThreads;
+        *reinterpret_cast<u32x4*>(buf + (p0 >> 4) * kKStride + 8 * (p0 & 15)) = S.k0;
+        *reinterpret_cast<u32x4*>(buf + (p1 >> 4) * kKStride + 8 * (p1 & 15)) = S.k1;
+        *reinterpret_cast<u32x4*>(buf + kKHalves + v_addr(p0 >> 3, 8 * (p0 & 7))) = S.v0;
+        *reinterpret_cast<u32x4*>(buf + kKHalves + v_addr(p1 >> 3, 8 * (p1 & 7))) = S.v1;
     };
 
     // ---- one chunk of attention for the current unit --------------------------
@@ -281,30 +319,42 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
                     for (int j = 0; j < 4; j++)
                         if (key0 + 16 * st2 + 4 * lg + j >= my_kend) s[h][st2][j] = -INFINITY;
         }
-        // Online softmax (m_run in log2 units) + P^T fragments.
-        f16x8 pb[kHeadsPerWave][kSub / 2];
+        // Online softmax (m_run in log2 units). Both heads' chunk maxima and the
+        // (rare) rescale come first, so that the exponentials, P^T packing and
+        // the P.V / row-sum MFMAs below form one block the scheduler can interleave.
+        float cm[kHeadsPerWave];
+        bool up[kHeadsPerWave];
 #pragma unroll
         for (int h = 0; h < kHeadsPerWave; h++) {
-            float cm = -INFINITY;
+            float v = -INFINITY;
 #pragma unroll
             for (int st2 = 0; st2 < kSub; st2++)
-                cm = fmaxf(cm, fmaxf(fmaxf(s[h][st2][0], s[h][st2][1]), fmaxf(s[h][st2][2], s[h][st2][3])));
-            cm = group_max(cm) * c2;
+                v = fmaxf(v, fmaxf(fmaxf(s[h][st2][0], s[h][st2][1]), fmaxf(s[h][st2][2], s[h][st2][3])));
+            cm[h] = group_max(v) * c2;
             // Lazy rescale: the running max of a row moves only when the chunk
             // max exceeds it by more than kLazy; p then stays below 2^kLazy,
             // which f16 P and the f32 accumulators hold as well as p <= 1.
-            const bool up = cm > m_run[h] + kLazy;
-            if (__any(up)) {
-                const float m_new = up ? cm : m_run[h];
-                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 from -inf
+            up[h] = cm[h] > m_run[h] + kLazy;
+        }
+        if (__any(up[0] || up[1])) {
+#pragma unroll
+            for (int h = 0; h < kHeadsPerWave; h++) {
+                const float m_new = up[h] ? cm[h] : m_run[h];
+                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 from -inf, 1 if kept
                 m_run[h] = m_new;
                 l_acc[h][0] *= alpha;   // only element 0 is read
 #pragma unroll
                 for (int dt = 0; dt < 8; dt++) o[h][dt] *= alpha;
             }
-            const float neg_m = -m_run[h];
+        }
+        // P^T fragments, row sums (ones x P^T on the matrix core, so they use the
+        // same f16-rounded P as O) and O^T += V^T P^T, per 32 keys.
 #pragma unroll
-            for (int kc = 0; kc < kSub / 2; kc++) {
+        for (int kc = 0; kc < kSub / 2; kc++) {
+            f16x8 pb[kHeadsPerWave];
+#pragma unroll
+            for (int h = 0; h < kHeadsPerWave; h++) {
+                const float neg_m = -m_run[h];
                 float p[8];
 #pragma unroll
                 for (int half = 0; half < 2; half++)
@@ -314,20 +364,14 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
                 U4 pk;
 #pragma unroll
                 for (int i = 0; i < 4; i++) pk.w[i] = pack2_rne(p[2 * i], p[2 * i + 1]);
-                pb[h][kc] = __builtin_bit_cast(f16x8, pk);
-                // Row sum on the matrix core: ones x P^T sums the (rounded) P of
-                // each token over the 32 keys, in every row of the result.
-                l_acc[h] = mfma16(ones8, pb[h][kc], l_acc[h]);
+                pb[h] = __builtin_bit_cast(f16x8, pk);
+                l_acc[h] = mfma16(ones8, pb[h], l_acc[h]);
             }
-        }
-        // O^T += V^T P^T: per k-step 16 independent MFMAs.
-#pragma unroll
-        for (int kc = 0; kc < kSub / 2; kc++) {
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 const f16x8 va = *reinterpret_cast<const f16x8*>(vb + v_addr(16 * dt + lr, 32 * kc + 8 * lg));
 #pragma unroll
-                for (int h = 0; h < kHeadsPerWave; h++) o[h][dt] = mfma16(va, pb[h][kc], o[h][dt]);
+                for (int h = 0; h < kHeadsPerWave; h++) o[h][dt] = mfma16(va, pb[h], o[h][dt]);
             }
         }
     };
@@ -406,8 +450,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
+    hipLaunchKernelGGL(kv_dequant_kernel, dim3((a.n_rows + kChunk - 1) / kChunk, n_kv_head), dim3(256), 0, s, a);
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
-    hipLaunchKernelGGL(prefill_kernel, dim3(n_pairs, n_kv_head), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(prefill_kernel, dim3(n_pairs * n_kv_head), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

@@ -38,6 +38,7 @@ struct bp_model {
     uint16_t* rope_cs;
     float* partials;
     uint64_t partials_floats;
+    uint16_t* kv16;       // prefill: f16 image of one layer's K and V (prefill_image_bytes)
     uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
@@ -254,7 +255,8 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
     if (hipMalloc(&m->kv_k, m->kv_bytes) != hipSuccess || hipMalloc(&m->kv_v, m->kv_bytes) != hipSuccess ||
         hipMalloc(&m->rope_cs, rope_elems * 2) != hipSuccess ||
         hipMalloc(&m->partials, m->partials_floats * 4) != hipSuccess ||
-        hipMalloc(&m->q_norm, static_cast<size_t>(cfg->n_head) * cfg->head_dim * 2) != hipSuccess) {
+        hipMalloc(&m->q_norm, static_cast<size_t>(cfg->n_head) * cfg->head_dim * 2) != hipSuccess ||
+        hipMalloc(&m->kv16, bp::prefill_image_bytes(cfg->n_kv_head, max_seq)) != hipSuccess) {
         (void)hipGetLastError();
         return bail(fail(BP_ERR_OUT_OF_MEMORY, "hipMalloc failed for KV cache of %llu bytes x2",
                          static_cast<unsigned long long>(m->kv_bytes)));
@@ -278,6 +280,7 @@ void bp_model_destroy(bp_model* m) {
         if (m->kv_v) (void)hipFree(m->kv_v);
         if (m->rope_cs) (void)hipFree(m->rope_cs);
         if (m->partials) (void)hipFree(m->partials);
+        if (m->kv16) (void)hipFree(m->kv16);
         if (m->q_norm) (void)hipFree(m->q_norm);
     }
     (void)hipGetLastError();
@@ -460,6 +463,10 @@ bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t
     a.causal = is_prefill ? 1u : 0u;
     a.n_tiles = (m_tokens + bp::kPrefillTileTok - 1) / bp::kPrefillTileTok;
     a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:524
+    a.ws_chunks = (m->max_seq + 63) / 64;
+    a.k16 = m->kv16;
+    a.vt16 = m->kv16 + bp::prefill_image_bytes(m->cfg.n_kv_head, m->max_seq) / 4;
+    a.n_rows = static_cast<uint32_t>(rows);
     return hip_check(m, bp::launch_prefill(a, m->cfg.n_kv_head, m->stream), "attention launch");
 }
 

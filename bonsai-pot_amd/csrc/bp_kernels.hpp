@@ -82,7 +82,19 @@ struct PrefillArgs {
     uint32_t causal;          // 1: token m sees rows [0, pos+m]; 0: rows [0, pos)
     uint32_t n_tiles;         // ceil(m_tokens / kPrefillTileTok)
     float scale;
+    // f16 image of the layer's K and V, written by the dequantization pass for
+    // rows [0, n_rows) (zeros up to the next 64-row chunk), per KV head g:
+    // K  at k16  + (g * ws_chunks + c) * 64 * 128: rows of chunk c, row-major;
+    // V^T at vt16 + (g * ws_chunks + c) * 128 * 64: dims of chunk c, slot-major.
+    uint16_t* k16;
+    uint16_t* vt16;
+    uint32_t ws_chunks;       // 64-row chunks per KV head in the image
+    uint32_t n_rows;          // rows the queries attend: cur of the last token
 };
+// Bytes of the f16 K/V image for max_seq rows (one layer, both tensors).
+inline uint64_t prefill_image_bytes(uint32_t n_kv_head, uint32_t max_seq) {
+    return 2ull * n_kv_head * ((max_seq + 63) / 64) * 64 * 128 * 2;
+}
 
 hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t m_tokens,
                               hipStream_t s);

@@ -49,11 +49,9 @@ constexpr int kThreads = 512;
 constexpr int kHeadsPerWave = 2;
 constexpr int kChunk = 64;               // cache rows per LDS chunk
 constexpr int kSub = kChunk / 16;        // 16-row S^T sub-tiles per chunk
-constexpr int kKStride = kHeadDim + 8;   // halves per K row in LDS (pad vs bank conflicts)
-constexpr int kVStride = kChunk + 8;     // halves per V^T row in LDS
-constexpr int kKHalves = kChunk * kKStride;
-constexpr int kVHalves = kHeadDim * kVStride;
-constexpr int kBufHalves = kKHalves + kVHalves;   // one staged chunk
+constexpr int kKHalves = kChunk * kHeadDim;   // K rows, 256 B each
+constexpr int kVHalves = kHeadDim * kChunk;   // V^T rows (dims), 128 B each
+constexpr int kBufHalves = kKHalves + kVHalves;   // one staged chunk (32 KB)
 constexpr float kLazy = 8.0f;            // lazy-rescale threshold (log2 units)
 
 struct alignas(16) U4 { uint32_t w[4]; };
@@ -70,10 +68,15 @@ __device__ __forceinline__ int v_slot(int key) {
     const int s = k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3);
     return (key & 32) + s;
 }
-// Half-word offset of (V^T row, slot) in LDS: 16-byte group (slot >> 3) is
-// XOR-swizzled with (row >> 3) & 7.
-__device__ __forceinline__ int v_addr(int row, int slot) {
-    return row * kVStride + 8 * ((slot >> 3) ^ ((row >> 3) & 7)) + (slot & 7);
+// Bank-conflict swizzles of the staged chunk (no padding, so that the image
+// in global memory is the LDS image and a chunk is one linear copy):
+// 16-byte group j of K row r sits at group j ^ (r & 15); group j of V^T row
+// (dim) d at group j ^ (d & 7).
+__device__ __forceinline__ int k_addr(int row, int group) {
+    return row * kHeadDim + 8 * (group ^ (row & 15));
+}
+__device__ __forceinline__ int v_addr(int dim, int group) {
+    return dim * kChunk + 8 * (group ^ (dim & 7));
 }
 
 // Reductions across the 4 lane groups of a token column (lanes l, l^16,
@@ -148,9 +151,10 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
             w[2 * i] = deq(x, 0x04010400u, kd, kc);
             w[2 * i + 1] = deq(x, 0x04030402u, kd, kc);
         }
-        U4* kdst = reinterpret_cast<U4*>(a.k16 + ((static_cast<uint64_t>(g) * a.ws_chunks + c) * kChunk + kr) * kHeadDim + 32 * kb);
+        uint16_t* kdst = a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves;
 #pragma unroll
-        for (int i = 0; i < 4; i++) kdst[i] = U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
+        for (int i = 0; i < 4; i++)
+            *reinterpret_cast<U4*>(kdst + k_addr(kr, 4 * kb + i)) = U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
     }
     // ---- V^T through LDS ----
     {
@@ -175,9 +179,10 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
     __syncthreads();
     // V^T rows: thread t -> dim t >> 1, slots 32 (t & 1) .. +32.
     const int dim = t >> 1, s0 = 32 * (t & 1);
-    uint16_t* vdst = a.vt16 + ((static_cast<uint64_t>(g) * a.ws_chunks + c) * kHeadDim + dim) * kChunk + s0;
+    uint16_t* vdst = a.vt16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kVHalves;
 #pragma unroll
-    for (int i = 0; i < 4; i++) *reinterpret_cast<U4*>(vdst + 8 * i) = *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
+    for (int i = 0; i < 4; i++)
+        *reinterpret_cast<U4*>(vdst + v_addr(dim, (s0 >> 3) + i)) = *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
 }
 
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
@@ -262,27 +267,23 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // the second half of it); B waves on tile B.
     start_unit(is_b || n_a == 0 ? tile_b : tile_a);
 
-    // ---- staging: copy a chunk's f16 K rows and V^T from the image -------------
-    // 32 KB per chunk = 4 16-byte pieces per thread: K piece p (= t, t + 512) is
-    // row p >> 4, dims 8 (p & 15) ..; V^T piece p is dim p >> 3, slots 8 (p & 7) ..
-    const uint16_t* k16 = a.k16 + static_cast<uint64_t>(g) * a.ws_chunks * kChunk * kHeadDim;
-    const uint16_t* vt16 = a.vt16 + static_cast<uint64_t>(g) * a.ws_chunks * kHeadDim * kChunk;
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    struct Stage { u32x4 k0, k1, v0, v1; };   // vector members: kept in registers
-    auto load_chunk = [&](Stage& S, uint32_t c) {
-        const u32x4* kc = reinterpret_cast<const u32x4*>(k16 + static_cast<uint64_t>(c) * kChunk * kHeadDim);
-        const u32x4* vc = reinterpret_cast<const u32x4*>(vt16 + static_cast<uint64_t>(c) * kHeadDim * kChunk);
-        S.k0 = kc[t];
-        S.k1 = kc[t + kThreads];
-        S.v0 = vc[t];
-        S.v1 = vc[t + kThreads];
-    };
-    auto store_chunk = [&](const Stage& S, uint16_t* buf) {
-        const int p0 = t, p1 = t + kThreads;
-        *reinterpret_cast<u32x4*>(buf + (p0 >> 4) * kKStride + 8 * (p0 & 15)) = S.k0;
-        *reinterpret_cast<u32x4*>(buf + (p1 >> 4) * kKStride + 8 * (p1 & 15)) = S.k1;
-        *reinterpret_cast<u32x4*>(buf + kKHalves + v_addr(p0 >> 3, 8 * (p0 & 7))) = S.v0;
-        *reinterpret_cast<u32x4*>(buf + kKHalves + v_addr(p1 >> 3, 8 * (p1 & 7))) = S.v1;
+    // ---- staging: a chunk's K rows and V^T (32 KB, already swizzled in the
+    // image) copied straight into LDS by global_load_lds (no registers): wave
+    // w's copy k (0..3) moves 1 KB, pieces 512 k + 64 w + lane. -------------------
+    const uint16_t* k16 = a.k16 + static_cast<uint64_t>(g) * a.ws_chunks * kKHalves;
+    const uint16_t* vt16 = a.vt16 + static_cast<uint64_t>(g) * a.ws_chunks * kVHalves;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    auto load_chunk = [&](uint16_t* buf, uint32_t c) {
+        const uint16_t* ks = k16 + static_cast<uint64_t>(c) * kKHalves;
+        const uint16_t* vs = vt16 + static_cast<uint64_t>(c) * kVHalves;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int piece = 512 * (k & 1) + 64 * wv;   // 16-byte pieces within K or V^T
+            const uint16_t* src = (k < 2 ? ks : vs) + 8 * (piece + lane);
+            uint16_t* dst = buf + (k < 2 ? 0 : kKHalves) + 8 * piece;
+            __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
+                                             (void __attribute__((address_space(3)))*)dst, 16, 0, 0);
+        }
     };
 
     // ---- one chunk of attention for the current unit --------------------------
@@ -301,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             f16x8 ka[kSub];
 #pragma unroll
             for (int st2 = 0; st2 < kSub; st2++)
-                ka[st2] = *reinterpret_cast<const f16x8*>(kb + (16 * st2 + lr) * kKStride + 32 * kk + 8 * lg);
+                ka[st2] = *reinterpret_cast<const f16x8*>(kb + k_addr(16 * st2 + lr, 4 * kk + lg));
 #pragma unroll
             for (int st2 = 0; st2 < kSub; st2++)
 #pragma unroll
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             }
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
-                const f16x8 va = *reinterpret_cast<const f16x8*>(vb + v_addr(16 * dt + lr, 32 * kc + 8 * lg));
+                const f16x8 va = *reinterpret_cast<const f16x8*>(vb + v_addr(16 * dt + lr, 4 * kc + lg));
 #pragma unroll
                 for (int h = 0; h < kHeadsPerWave; h++) o[h][dt] = mfma16(va, pb[h], o[h][dt]);
             }
@@ -381,17 +382,17 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     auto c1_of = [&](uint32_t i) { return i; };                      // valid while i < mid
     auto has2 = [&](uint32_t i) { return i >= n_a && mid + (i - n_a) < n_b; };
     auto c2_of = [&](uint32_t i) { return mid + (i - n_a); };
-    Stage s1, s2;
-    load_chunk(s1, c1_of(0));
-    if (has2(0)) load_chunk(s2, c2_of(0));
-    store_chunk(s1, lds[0][0]);
-    if (has2(0)) store_chunk(s2, lds[1][0]);
+    // A copy into LDS completes when the issuing wave's vmcnt drains; the
+    // barrier after that wait publishes it to the workgroup.
+    load_chunk(lds[0][0], c1_of(0));
+    if (has2(0)) load_chunk(lds[1][0], c2_of(0));
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (uint32_t i = 0; i < n_iter; i++) {
         const int buf = i & 1;
         const bool next = i + 1 < n_iter, next2 = next && has2(i + 1);
-        if (next) load_chunk(s1, c1_of(i + 1));
-        if (next2) load_chunk(s2, c2_of(i + 1));
+        if (next) load_chunk(lds[0][buf ^ 1], c1_of(i + 1));
+        if (next2) load_chunk(lds[1][buf ^ 1], c2_of(i + 1));
         // One call site: a wave computes stream 1 (B waves; A waves while on
         // tile A) or stream 2 (A waves once on B's second half).
         const bool on1 = is_b || i < n_a;
@@ -402,8 +403,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             write_unit();
             start_unit(tile_b);
         }
-        if (next) store_chunk(s1, lds[0][buf ^ 1]);
-        if (next2) store_chunk(s2, lds[1][buf ^ 1]);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 

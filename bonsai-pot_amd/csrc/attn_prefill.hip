@@ -79,19 +79,9 @@ __device__ __forceinline__ int v_addr(int dim, int group) {
     return dim * kChunk + 8 * (group ^ (dim & 7));
 }
 
-// Reductions across the 4 lane groups of a token column (lanes l, l^16,
-// l^32, l^48): xor 16 by ds_swizzle (bit mode), xor 32 by ds_bpermute.
-__device__ __forceinline__ float swz_xor16(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-}
-__device__ __forceinline__ float group_max(float v) {
-    v = fmaxf(v, swz_xor16(v));
-    return fmaxf(v, __shfl_xor(v, 32));
-}
-__device__ __forceinline__ float group_sum(float v) {
-    v += swz_xor16(v);
-    return v + __shfl_xor(v, 32);
-}
+// Maximum across the 4 lane groups of a token column (lanes l, l^16, l^32,
+// l^48), by lane-row swaps (no LDS round trip).
+__device__ __forceinline__ float group_max(float v) { return max_xor32(max_xor16(v)); }
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -287,8 +277,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     };
 
     // ---- one chunk of attention for the current unit --------------------------
-    auto compute = [&](const uint16_t* buf, uint32_t key0) {
-        if (!unit_live || key0 >= wave_kend) return;
+    // `issue` starts the copies of the next chunks; it runs once per call, in
+    // the shadow of the q.k MFMAs (a copy's issue waits on the memory pipeline).
+    auto compute = [&](const uint16_t* buf, uint32_t key0, auto&& issue) {
+        if (!unit_live || key0 >= wave_kend) { issue(); return; }
         const uint16_t* kb = buf;
         const uint16_t* vb = buf + kKHalves;
         // S^T = K Q^T, k-step outer: each step issues 8 independent MFMAs.
@@ -308,6 +300,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int h = 0; h < kHeadsPerWave; h++) s[h][st2] = mfma16(ka[st2], qb[h][kk], s[h][st2]);
         }
+        issue();
         // Mask (only chunks that reach past the unit's earliest visible row);
         // raw scores, the scale is applied inside the exponent.
         const bool need_mask = key0 + kChunk > (a.causal ? a.pos + wtok0 + 1 : a.pos);
@@ -391,12 +384,15 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     for (uint32_t i = 0; i < n_iter; i++) {
         const int buf = i & 1;
         const bool next = i + 1 < n_iter, next2 = next && has2(i + 1);
-        if (next) load_chunk(lds[0][buf ^ 1], c1_of(i + 1));
-        if (next2) load_chunk(lds[1][buf ^ 1], c2_of(i + 1));
+        auto issue = [&]() {
+            if (next) load_chunk(lds[0][buf ^ 1], c1_of(i + 1));
+            if (next2) load_chunk(lds[1][buf ^ 1], c2_of(i + 1));
+        };
         // One call site: a wave computes stream 1 (B waves; A waves while on
         // tile A) or stream 2 (A waves once on B's second half).
         const bool on1 = is_b || i < n_a;
-        if (on1 || has2(i)) compute(lds[on1 ? 0 : 1][buf], (on1 ? c1_of(i) : c2_of(i)) * kChunk);
+        if (on1 || has2(i)) compute(lds[on1 ? 0 : 1][buf], (on1 ? c1_of(i) : c2_of(i)) * kChunk, issue);
+        else issue();
         if (!is_b && i + 1 == n_a) {   // tile A done: store it, move to B's second half
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++) l_run[h] = l_acc[h][0];

@@ -29,6 +29,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Lane exchanges across 16- and 32-lane rows without LDS: v_permlane16_swap /
+// v_permlane32_swap of a register with itself leave, in every lane, the pair
+// {v[l], v[l ^ 16]} (resp. {v[l], v[l ^ 32]}) in the two results, in an order
+// that depends on the row; max and sum of the pair do not depend on it.
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
+    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
+    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
+}
+
 // Sign-extend byte `i` of a packed word to float (exact).
 __device__ __forceinline__ float i8f(uint32_t w, int i) {
     return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * i)) >> 24);

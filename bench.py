@@ -282,17 +282,17 @@ def cpu_baseline(seconds=10.0):
 
 def roofline_decode(d4):
     """Dominant kernel pair of the headline step: decode_split_kernel<true, 1> +
-    decode_merge_kernel<true>, i.e. one layer of the fused decode step.
+    decode_merge_kernel<true, 8>, i.e. one layer of the fused decode step.
     achieved = algorithmic bytes of one layer (4097 rows x 2304 B + q in/out)
     / the per-layer time of the timed region (HIP events, graph replays)."""
     per_layer_s = d4["ms_per_step"] * 1e-3 / d4["layers"]
     achieved = d4["kernel_bytes"] / per_layer_s / 1e9
     split = measured_traffic("decode4k", "decode_split_kernel<true, 1>")
-    merge = measured_traffic("decode4k", "decode_merge_kernel<true>")
+    merge = measured_traffic("decode4k", "decode_merge_kernel<true, 8>")
     traffic = None if split is None or merge is None else split + merge
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-            "kernel": "decode_split_kernel<true, 1> + decode_merge_kernel<true> (one layer of the fused step)",
+            "kernel": "decode_split_kernel<true, 1> + decode_merge_kernel<true, 8> (one layer of the fused step)",
             "bytes_per_launch": d4["kernel_bytes"], "us_per_launch": per_layer_s * 1e6}
 
 

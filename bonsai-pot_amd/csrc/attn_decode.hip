@@ -92,15 +92,9 @@ template <int kCtrl>
 __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
 }
-__device__ __forceinline__ float swz_xor16(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-}
 // Sum over lanes l, l^8, l^16, l^32.
 __device__ __forceinline__ float sum_slots(float v) {
-    v += dpp_f<0x128>(v);
-    v += swz_xor16(v);
-    v += __shfl_xor(v, 32);
-    return v;
+    return sum_xor32(sum_xor16(v + dpp_f<0x128>(v)));   // row_ror:8 == xor 8 within 16 lanes
 }
 
 template <bool kFused, int kH>
@@ -275,8 +269,7 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
             for (int j = 0; j < 4; j++) s[j] = r0 + j < row_end ? s[j] : -INFINITY;
         }
         float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        bm = fmaxf(bm, swz_xor16(bm));
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        bm = max_xor32(max_xor16(bm));
         const float m_new = fmaxf(m_run, bm);
         if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
             const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);   // 0 on the first batch
@@ -354,10 +347,8 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
 
     // ---- per-wave totals: l and the W column sums over the 4 row groups; O of
     // head lg, dims 8 lr .. +8 minus the 1152 bias of V -----------------------
-    lsum += swz_xor16(lsum);
-    lsum += __shfl_xor(lsum, 32);
-    float bs = bsum + swz_xor16(bsum);
-    bs += __shfl_xor(bs, 32);
+    lsum = sum_xor32(sum_xor16(lsum));
+    const float bs = sum_xor32(sum_xor16(bsum));
     const float bias = 1152.0f * __shfl(bs, 4 * lg + (lr >> 2));
     {
         float ov[8];
@@ -407,8 +398,9 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     if (t % kTpH == 0) *reinterpret_cast<float2*>(part + kHeadDim) = make_float2(M, L);
 }
 
-// One wave per (query head, 32-dim chunk).
-template <bool kFused>
+// One wave per (query head, 32-dim chunk); kLoads = 8 (up to 64 splits) or
+// 16 (up to 128) partial loads per lane.
+template <bool kFused, int kLoads>
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
     const int lane = threadIdx.x;
     const uint32_t h = blockIdx.x >> 2, c = blockIdx.x & 3;
@@ -419,16 +411,17 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
 
     // O chunk loads: lane -> splits (lane >> 3) + 8i, dims 32c + 4 (lane & 7) .. +3.
     const int f4 = lane & 7;
-    float4 ov[kMaxSplits / 8];
+    float4 ov[kLoads];
 #pragma unroll
-    for (int i = 0; i < kMaxSplits / 8; i++) {
+    for (int i = 0; i < kLoads; i++) {
         const uint32_t s = min(static_cast<uint32_t>((lane >> 3) + 8 * i), ns - 1);
         ov[i] = *reinterpret_cast<const float4*>(ph + static_cast<uint64_t>(s) * kPartStride + 32 * c + 4 * f4);
     }
     // (m, l) of splits lane and lane + 64.
     const uint32_t ls0 = min(static_cast<uint32_t>(lane), ns - 1), ls1 = min(static_cast<uint32_t>(lane) + 64u, ns - 1);
     const float2 ml0 = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls0) * kPartStride + kHeadDim);
-    const float2 ml1 = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls1) * kPartStride + kHeadDim);
+    float2 ml1 = make_float2(-INFINITY, 0.0f);
+    if constexpr (kLoads > 8) ml1 = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls1) * kPartStride + kHeadDim);
     const float m_s0 = static_cast<uint32_t>(lane) < ns ? ml0.x : -INFINITY;
     const float m_s1 = static_cast<uint32_t>(lane) + 64u < ns ? ml1.x : -INFINITY;
 
@@ -463,7 +456,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
 
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int i = 0; i < kMaxSplits / 8; i++) {
+    for (int i = 0; i < kLoads; i++) {
         const float wi = __shfl(i < 8 ? w0 : w1, (lane >> 3) + 8 * (i & 7));
         acc.x = __builtin_fmaf(wi, ov[i].x, acc.x);
         acc.y = __builtin_fmaf(wi, ov[i].y, acc.y);
@@ -530,16 +523,24 @@ static void launch_split(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s)
                            dim3(SplitShape<1>::kThreads), 0, s, a);
 }
 
+template <bool kFused>
+static void launch_merge(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
+    if (a.n_splits > 64)
+        hipLaunchKernelGGL((decode_merge_kernel<kFused, 16>), dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_merge_kernel<kFused, 8>), dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
+}
+
 hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
     launch_split<false>(a, n_kv_head, s);
     if (a.n_splits > 1)
-        hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
+        launch_merge<false>(a, n_kv_head, s);
     return hipGetLastError();
 }
 
 hipError_t launch_decode_step(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
     launch_split<true>(a, n_kv_head, s);
-    hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
+    launch_merge<true>(a, n_kv_head, s);
     return hipGetLastError();
 }
 

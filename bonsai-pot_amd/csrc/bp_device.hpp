@@ -33,22 +33,25 @@ __device__ __forceinline__ float wave_sum(float v) {
 // v_permlane32_swap of a register with itself leave, in every lane, the pair
 // {v[l], v[l ^ 16]} (resp. {v[l], v[l ^ 32]}) in the two results, in an order
 // that depends on the row; max and sum of the pair do not depend on it.
-__device__ __forceinline__ float max_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+// (The results are copied to scalars before the bit casts: a bit cast of a
+// vector element directly is miscompiled to element 0.)
+struct LanePair { float a, b; };
+__device__ __forceinline__ LanePair xchg16(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return {__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
 }
-__device__ __forceinline__ float max_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+__device__ __forceinline__ LanePair xchg32(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return {__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
 }
-__device__ __forceinline__ float sum_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
-    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-}
-__device__ __forceinline__ float sum_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
-    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-}
+__device__ __forceinline__ float max_xor16(float v) { const LanePair p = xchg16(v); return fmaxf(p.a, p.b); }
+__device__ __forceinline__ float max_xor32(float v) { const LanePair p = xchg32(v); return fmaxf(p.a, p.b); }
+__device__ __forceinline__ float sum_xor16(float v) { const LanePair p = xchg16(v); return p.a + p.b; }
+__device__ __forceinline__ float sum_xor32(float v) { const LanePair p = xchg32(v); return p.a + p.b; }
 
 // Sign-extend byte `i` of a packed word to float (exact).
 __device__ __forceinline__ float i8f(uint32_t w, int i) {

@@ -2,14 +2,19 @@
 //
 // Same result as src/shaders/attention.wgsl (reference repository) — token m
 // attends rows [0, cur) with cur = causal ? pos + m + 1 : pos, f32 softmax,
-// f16 output — computed as a flash-attention over LDS tiles:
+// f16 output — computed in two passes:
 //
+// kv_dequant_kernel writes the layer's K and V for rows [0, cur of the last
+// token) as an f16 image (f16(d * q) per value): per KV head and 64-row chunk,
+// K rows and V^T (dims x key slots in the MFMA order below), 16-byte groups
+// XOR-swizzled against LDS bank conflicts, so that a chunk is one linear copy.
+//
+// prefill_kernel, a flash-attention over LDS tiles of that image:
 //  * Query tokens form tiles of 32; a "unit" is 16 tokens x 2 GQA heads (one
 //    wave's MFMA columns). A 512-thread workgroup owns one KV head and a
-//    zig-zag PAIR of tiles: light tile A = blockIdx.x, heavy tile
-//    B = n_tiles-1-blockIdx.x. Wave w (SIMD w & 3) owns unit (w & 3) of tile
-//    A if w < 4, of tile B otherwise, so each SIMD holds one A wave and one B
-//    wave (one's softmax overlaps the other's MFMAs).
+//    zig-zag PAIR of tiles: light tile A = p, heavy tile B = n_tiles-1-p
+//    (1-D grid, KV head fastest: one head per XCD). Wave w (SIMD w & 3) owns
+//    unit (w & 3) of tile A if w < 4, of tile B otherwise.
 //  * Work balance (split-K inside the workgroup): with n_A / n_B the 64-row
 //    chunks tiles A / B attend and mid = ceil((n_A + n_B) / 2), the B waves
 //    take B's chunks [0, mid) while the A waves take A's chunks [0, n_A) and
@@ -18,18 +23,17 @@
 //    with two busy waves per SIMD, so the 256 CUs finish together. (A middle
 //    tile paired with itself is simply split between its two waves.)
 //  * Chunks are staged from two streams — stream 1 serves chunk i (A waves
-//    while i < n_A, B waves), stream 2 serves B's chunk mid + i - n_A — each
-//    dequantized from Q8_0 to f16 (d * q, one rounding) into double-buffered
-//    LDS: K row-major, V transposed (dim-major, 16-byte groups XOR-swizzled by
-//    row against bank conflicts), so both MFMA operands are single 16-byte
-//    LDS reads. Loads for iteration i+1 are in flight while i is computed.
+//    while i < n_A, B waves), stream 2 serves B's chunk mid + i - n_A — copied
+//    from the image straight into double-buffered LDS by global_load_lds (no
+//    registers), so both MFMA operands are single 16-byte LDS reads. The
+//    copies for iteration i+1 are issued during iteration i's q.k MFMAs.
 //  * S^T = K Q^T with v_mfma_f32_16x16x32_f16 (K = 32 dims per step): the
 //    output fragment of lane l holds 8 keys of token (l % 16) per 32 keys. With
 //    the keys stored in V^T in the matching permuted order, those fragments are
 //    directly the B operand of O^T = V^T P^T — no shuffles, no LDS trip.
 //  * Online softmax in the exp2 domain (p = exp2(s * scale * log2 e - m) is
-//    one FMA and one exp), row max across the 4 lane groups by
-//    swizzle/permute, and a lazy running max (moved only by more than kLazy
+//    one FMA and one exp), row max across the 4 lane groups by lane-row
+//    swaps (v_permlane16/32_swap), and a lazy running max (moved only by more than kLazy
 //    log2 units), so the O accumulators are almost never touched by VALU.
 //
 // MFMA fragment layout used (v_mfma_f32_16x16x32_f16, lane l, g = l / 16):

@@ -43,6 +43,12 @@ _preload_torch_hip_runtime()
 lib = ctypes.CDLL(library_path)
 
 
+class MatvecRange(ctypes.Structure):
+    """bp_matvec_range: one Q1_0 tensor of a fused normed matvec."""
+    _fields_ = [("d_offset", ctypes.c_uint32), ("qs_offset", ctypes.c_uint32), ("n", ctypes.c_uint32),
+                ("output_offset", ctypes.c_uint32)]
+
+
 class _Config(ctypes.Structure):
     _fields_ = [("n_layer", ctypes.c_uint32), ("n_head", ctypes.c_uint32),
                 ("n_kv_head", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
@@ -66,6 +72,10 @@ _SIGS = {
     "bp_dispatch_attention_decode_step": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                                   _u32]),
     "bp_dispatch_attention": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_matvec_q1_0": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_matvec_q1_0_silu": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_matvec_q1_0_fused_normed": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                                     ctypes.POINTER(MatvecRange)]),
     "bp_kv_snapshot_payload_bytes": (_u64, [_u32, _u32, _u32]),
     "bp_kv_snapshot_capture": (_i32, [_vp, _u32, _vp, _u64]),
     "bp_kv_snapshot_apply": (_i32, [_vp, _u32, _vp, _u64]),
@@ -171,6 +181,25 @@ class Model:
                            m_tokens: int, is_prefill: bool) -> None:
         _check(lib.bp_dispatch_attention(self._h, act, q_off, out_off, layer_il, pos, m_tokens,
                                          1 if is_prefill else 0))
+
+    # -- Q1_0 decode matvecs (src/forward.rs:212-334) -----------------------------
+    # `weights` and `act` are device pointers (ints); w_d / w_qs byte offsets.
+    def dispatch_matvec_q1_0(self, weights: int, act: int, k: int, n: int, w_d: int, w_qs: int,
+                             in_off: int, out_off: int, accumulate: bool) -> None:
+        _check(lib.bp_dispatch_matvec_q1_0(self._h, weights, act, k, n, w_d, w_qs, in_off, out_off,
+                                           1 if accumulate else 0))
+
+    def dispatch_matvec_q1_0_silu(self, weights: int, act: int, k: int, n: int, w_d: int, w_qs: int,
+                                  gate_off: int, up_off: int, out_off: int, accumulate: bool) -> None:
+        _check(lib.bp_dispatch_matvec_q1_0_silu(self._h, weights, act, k, n, w_d, w_qs, gate_off, up_off,
+                                                out_off, 1 if accumulate else 0))
+
+    def dispatch_matvec_q1_0_fused_normed(self, weights: int, act: int, w_norms: int, k: int,
+                                          input_offset: int, w_norm_off: int, ranges) -> None:
+        """ranges: sequence of (d_offset, qs_offset, n, output_offset), 2 or 3 of them."""
+        arr = (MatvecRange * max(1, len(ranges)))(*[MatvecRange(*r) for r in ranges])
+        _check(lib.bp_dispatch_matvec_q1_0_fused_normed(self._h, weights, act, w_norms, k, input_offset,
+                                                        w_norm_off, len(ranges), arr))
 
     # -- snapshot payload (src/kv_snapshot.rs:203-372) ----------------------------
     def snapshot_payload(self, pos: int) -> bytes:

@@ -470,6 +470,87 @@ bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t
     return hip_check(m, bp::launch_prefill(a, m->cfg.n_kv_head, m->stream), "attention launch");
 }
 
+static bp_status matvec_common(bp_model* m, const void* weights, void* act, uint32_t k,
+                               bp::MatvecArgs& a) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!weights || !act) return fail(BP_ERR_INVALID_ARG, "weights/act is NULL");
+    if (k == 0 || k % 128 != 0 || k > bp::matvec_max_k())
+        return fail(BP_ERR_INVALID_ARG, "matvec k = %u must be a positive multiple of 128 <= %u", k,
+                    bp::matvec_max_k());
+    a.weights = static_cast<const uint8_t*>(weights);
+    a.act = static_cast<uint16_t*>(act);
+    a.k = k;
+    a.eps = m->cfg.rms_eps;
+    return BP_OK;
+}
+
+static bp_status matvec_check_tensor(uint32_t w_d, uint32_t w_qs) {
+    if ((w_d & 1u) || (w_qs & 3u))
+        return fail(BP_ERR_INVALID_ARG, "Q1_0 offsets: d must be 2-byte, qs 4-byte aligned (%u, %u)", w_d, w_qs);
+    return BP_OK;
+}
+
+bp_status bp_dispatch_matvec_q1_0(bp_model* m, const void* weights, void* act, uint32_t k, uint32_t n,
+                                  uint32_t w_d, uint32_t w_qs, uint32_t in_off, uint32_t out_off,
+                                  uint32_t accumulate) {
+    bp::MatvecArgs a{};
+    bp_status st = matvec_common(m, weights, act, k, a);
+    if (st != BP_OK) return st;
+    if (n == 0) return BP_OK;
+    if ((st = matvec_check_tensor(w_d, w_qs)) != BP_OK) return st;
+    if (in_off & 7u) return fail(BP_ERR_INVALID_ARG, "matvec in_off %u must be a multiple of 8", in_off);
+    a.n_total = n;
+    a.input_offset = in_off;
+    a.accumulate = accumulate ? 1u : 0u;
+    a.range[0] = {w_d, w_qs, n, out_off};
+    return hip_check(m, bp::launch_matvec_q1_0(a, 0, m->stream), "matvec_q1_0 launch");
+}
+
+bp_status bp_dispatch_matvec_q1_0_silu(bp_model* m, const void* weights, void* act, uint32_t k, uint32_t n,
+                                       uint32_t w_d, uint32_t w_qs, uint32_t gate_off, uint32_t up_off,
+                                       uint32_t out_off, uint32_t accumulate) {
+    bp::MatvecArgs a{};
+    bp_status st = matvec_common(m, weights, act, k, a);
+    if (st != BP_OK) return st;
+    if (n == 0) return BP_OK;
+    if ((st = matvec_check_tensor(w_d, w_qs)) != BP_OK) return st;
+    if ((gate_off | up_off) & 7u)
+        return fail(BP_ERR_INVALID_ARG, "matvec gate/up offsets (%u, %u) must be multiples of 8", gate_off, up_off);
+    a.n_total = n;
+    a.gate_offset = gate_off;
+    a.up_offset = up_off;
+    a.accumulate = accumulate ? 1u : 0u;
+    a.range[0] = {w_d, w_qs, n, out_off};
+    return hip_check(m, bp::launch_matvec_q1_0(a, 1, m->stream), "matvec_q1_0_silu launch");
+}
+
+bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* m, const void* weights, void* act, const void* w_norms,
+                                               uint32_t k, uint32_t in_off, uint32_t w_norm_off,
+                                               uint32_t n_ranges, const bp_matvec_range* ranges) {
+    bp::MatvecArgs a{};
+    bp_status st = matvec_common(m, weights, act, k, a);
+    if (st != BP_OK) return st;
+    if (!w_norms || !ranges) return fail(BP_ERR_INVALID_ARG, "w_norms/ranges is NULL");
+    if (n_ranges < 1 || n_ranges > 3) return fail(BP_ERR_INVALID_ARG, "n_ranges %u not in 1..3", n_ranges);
+    if ((in_off | w_norm_off) & 7u)
+        return fail(BP_ERR_INVALID_ARG, "matvec in_off / w_norm_off (%u, %u) must be multiples of 8", in_off, w_norm_off);
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < n_ranges; i++) {
+        if (ranges[i].n % 32 != 0)
+            return fail(BP_ERR_INVALID_ARG, "fused normed matvec range %u: n = %u not a multiple of 32", i, ranges[i].n);
+        if ((st = matvec_check_tensor(ranges[i].d_offset, ranges[i].qs_offset)) != BP_OK) return st;
+        a.range[i] = {ranges[i].d_offset, ranges[i].qs_offset, ranges[i].n, ranges[i].output_offset};
+        total += ranges[i].n;
+    }
+    if (total == 0) return BP_OK;
+    a.w_norms = static_cast<const uint16_t*>(w_norms);
+    a.n_total = static_cast<uint32_t>(total);
+    a.input_offset = in_off;
+    a.w_norm_off = w_norm_off;
+    return hip_check(m, bp::launch_matvec_q1_0(a, 2, m->stream), "matvec_q1_0_fused_normed launch");
+}
+
 static bp_status snapshot_copy(bp_model* m, uint32_t pos, uint8_t* payload, uint64_t payload_bytes,
                                bool to_host) {
     bp_status st = enter(m);

@@ -96,6 +96,28 @@ inline uint64_t prefill_image_bytes(uint32_t n_kv_head, uint32_t max_seq) {
     return 2ull * n_kv_head * ((max_seq + 63) / 64) * 64 * 128 * 2;
 }
 
+// Q1_0 matvec family (matvec_q1_0*.wgsl). Byte offsets into `weights`,
+// f16-element offsets into `act` / `w_norms` (inputs 8-element aligned).
+struct MatvecRange {
+    uint32_t d_offset, qs_offset, n, output_offset;
+};
+struct MatvecArgs {
+    const uint8_t* weights;
+    uint16_t* act;
+    const uint16_t* w_norms;  // normed mode only
+    uint32_t k;               // multiple of 128, <= matvec_max_k()
+    uint32_t n_total;         // rows over all ranges
+    uint32_t input_offset;    // plain / normed input x
+    uint32_t gate_offset, up_offset;   // silu mode input silu(gate) * up
+    uint32_t w_norm_off;
+    float eps;
+    uint32_t accumulate;      // plain / silu: y = f16(f32(y) + acc)
+    MatvecRange range[3];     // plain / silu: range[0] only; normed: multiples of 32 rows
+};
+// mode 0: matvec_q1_0, 1: matvec_q1_0_silu, 2: matvec_q1_0_fused_normed.
+hipError_t launch_matvec_q1_0(const MatvecArgs& a, int mode, hipStream_t s);
+uint32_t matvec_max_k();
+
 hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t m_tokens,
                               hipStream_t s);
 hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uint32_t m_tokens,

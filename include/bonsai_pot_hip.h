@@ -12,6 +12,10 @@
  *                                       src/forward.rs:820-857
  *   bp_dispatch_attention_decode_step <- the three above for one token (fused, 2 launches)
  *   bp_dispatch_attention            <- dispatch_attention           src/forward.rs:501-532
+ *   bp_dispatch_matvec_q1_0          <- dispatch_matvec_q1_0         src/forward.rs:212-241
+ *   bp_dispatch_matvec_q1_0_silu     <- dispatch_matvec_q1_0_silu    src/forward.rs:243-282
+ *   bp_dispatch_matvec_q1_0_fused_normed <- dispatch_matvec_q1_0_fused_normed
+ *                                       src/forward.rs:284-334
  *   bp_model_create / _destroy       <- KV / RoPE / partials part of Model::load_with_options
  *                                       src/model.rs:1148-1248
  *   bp_kv_snapshot_capture / _apply  <- kv_snapshot::capture / apply src/kv_snapshot.rs:203-372
@@ -135,6 +139,34 @@ bp_status bp_dispatch_attention_decode_step(bp_model* model, void* act, const vo
 bp_status bp_dispatch_attention(bp_model* model, void* act, uint32_t q_off, uint32_t out_off,
                                 uint32_t layer_il, uint32_t pos, uint32_t m_tokens,
                                 uint32_t is_prefill);
+
+/* Q1_0 decode matvec family (src/shaders/matvec_q1_0*.wgsl). `weights` is the
+ * device weight buffer; w_d / w_qs are BYTE offsets of a Q1_0 tensor in it
+ * (d: n x (k/128) f16, then qs: n x (k/128) x 16 bytes, 4-byte aligned,
+ * src/model.rs:784-804). k is a multiple of 128, at most 16384; activation
+ * offsets are f16-element offsets into `act` and must be multiples of 8.
+ * y[out_off + r] = f16(sum_b d[r][b] * sum_e (+-x[e])) (or, with accumulate,
+ * f16(f32(y) + that)), with the reference's f16 block accumulation. */
+bp_status bp_dispatch_matvec_q1_0(bp_model* model, const void* weights, void* act, uint32_t k,
+                                  uint32_t n, uint32_t w_d, uint32_t w_qs, uint32_t in_off,
+                                  uint32_t out_off, uint32_t accumulate);
+/* x = f16(silu(gate)) * up (silu in f32), gate / up at act[gate_off] / act[up_off]
+ * (src/shaders/matvec_q1_0_silu.wgsl, src/forward.rs:243-282). */
+bp_status bp_dispatch_matvec_q1_0_silu(bp_model* model, const void* weights, void* act, uint32_t k,
+                                       uint32_t n, uint32_t w_d, uint32_t w_qs, uint32_t gate_off,
+                                       uint32_t up_off, uint32_t out_off, uint32_t accumulate);
+/* One Q1_0 row range of the fused normed matvec: (d_offset, qs_offset, n, output_offset)
+ * (the ranges tuple of src/forward.rs:284-334). */
+typedef struct {
+    uint32_t d_offset, qs_offset, n, output_offset;
+} bp_matvec_range;
+/* rms_norm(x) * w_norm followed by 2 or 3 Q1_0 matvecs sharing x
+ * (src/shaders/matvec_q1_0_fused_normed.wgsl, src/forward.rs:284-334); every
+ * range's n is a multiple of 32 (the reference asks for 16). */
+bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* model, const void* weights, void* act,
+                                               const void* w_norms, uint32_t k, uint32_t in_off,
+                                               uint32_t w_norm_off, uint32_t n_ranges,
+                                               const bp_matvec_range* ranges);
 
 /* BONSAIKV v1 payload (src/kv_snapshot.rs:8-20): for kind in {K, V}, for each
  * layer: pos*(kv_dim/32)*4 bytes of d, then pos*kv_dim bytes of qs.

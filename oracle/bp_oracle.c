@@ -419,6 +419,131 @@ void bpo_attention(const bpo_attn_params* p, const uint16_t* act, const uint8_t*
 /* ------------------------------------------------------------------------- */
 /* Seeded inputs: splitmix64 -> uniform (53-bit) -> Box-Muller -> f16.        */
 /* ------------------------------------------------------------------------- */
+/* ---- Q1_0 decode matvecs ------------------------------------------------ */
+/* f64 -> f16, round to nearest even, subnormals kept. A sum or product of two
+ * f16 values is exact in f64, so f16 ops below round once, like the GPU's. */
+static uint16_t f64_to_f16(double v) {
+    const uint16_t sign = signbit(v) ? 0x8000u : 0u;
+    const double a = fabs(v);
+    if (isnan(v)) return sign | 0x7E00u;
+    if (a >= 65520.0) return sign | 0x7C00u;      /* the 65504 / 65536 tie goes to inf */
+    if (a < 6.103515625e-05) {                     /* below 2^-14: quantum 2^-24 */
+        const double r = nearbyint(a * 16777216.0);
+        return sign | (uint16_t)r;                 /* r = 1024 is the smallest normal */
+    }
+    int e;
+    (void)frexp(a, &e);                            /* a = m * 2^e, m in [0.5, 1) */
+    double r = nearbyint(ldexp(a, 11 - e));        /* [1024, 2048] */
+    if (r == 2048.0) { r = 1024.0; e += 1; }
+    const int E = e - 1 + 15;
+    if (E >= 31) return sign | 0x7C00u;
+    return (uint16_t)(sign | (uint16_t)(E << 10) | (uint16_t)((uint32_t)r - 1024u));
+}
+uint16_t bpo_f16_add(uint16_t a, uint16_t b) {
+    return f64_to_f16((double)bpo_f16_to_f32(a) + (double)bpo_f16_to_f32(b));
+}
+uint16_t bpo_f16_mul(uint16_t a, uint16_t b) {
+    return f64_to_f16((double)bpo_f16_to_f32(a) * (double)bpo_f16_to_f32(b));
+}
+
+/* matvec_q1_0.wgsl:88-111: one block, four f16 accumulators (component
+ * e mod 4, elements in increasing order), then f32(((c0 + c1) + c2) + c3). */
+static float q1_block_sum(const uint8_t* qs16, const uint16_t* x) {
+    uint16_t c[4] = {0, 0, 0, 0};
+    for (int w = 0; w < 4; w++) {
+        uint32_t q;
+        memcpy(&q, qs16 + 4 * w, 4);
+        for (int i = 0; i < 8; i++)
+            for (int cc = 0; cc < 4; cc++) {
+                const int e = 32 * w + 4 * i + cc;
+                const uint16_t xv = x[e];
+                const uint16_t v = ((q >> (4 * i + cc)) & 1u) ? xv : (uint16_t)(xv ^ 0x8000u);
+                c[cc] = bpo_f16_add(c[cc], v);
+            }
+    }
+    return bpo_f16_to_f32(bpo_f16_add(bpo_f16_add(bpo_f16_add(c[0], c[1]), c[2]), c[3]));
+}
+
+/* One row: lane t = block mod 8 accumulates acc_t = acc_t + d * sum over its
+ * blocks in order, then the xor 1, 2, 4 butterfly (matvec_q1_0.wgsl:112-123).
+ * dscale multiplies each block's f32 scale first (the fused normed inv_rms). */
+static float q1_row(const uint8_t* weights, uint32_t d_off, uint32_t qs_off, uint32_t k, uint32_t row,
+                    const uint16_t* x, int use_dscale, float dscale) {
+    const uint32_t nb = k / 128;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t b = 0; b < nb; b++) {
+        uint16_t dh;
+        memcpy(&dh, weights + d_off + ((uint64_t)row * nb + b) * 2, 2);
+        float d = bpo_f16_to_f32(dh);
+        if (use_dscale) d = d * dscale;
+        const float sum = q1_block_sum(weights + qs_off + ((uint64_t)row * nb + b) * 16, x + 128 * b);
+        const float term = d * sum;
+        acc[b % 8] = acc[b % 8] + term;
+    }
+    float s1[8], s2[8];
+    for (int t = 0; t < 8; t++) s1[t] = acc[t] + acc[t ^ 1];
+    for (int t = 0; t < 8; t++) s2[t] = s1[t] + s1[t ^ 2];
+    return s2[0] + s2[4];
+}
+
+static void q1_store(uint16_t* act, uint32_t yi, float acc, uint32_t accumulate) {
+    act[yi] = accumulate ? bpo_f32_to_f16(bpo_f16_to_f32(act[yi]) + acc) : bpo_f32_to_f16(acc);
+}
+
+void bpo_matvec_q1_0(const bpo_matvec_params* p, const uint8_t* weights, uint16_t* act) {
+    uint16_t* x = (uint16_t*)malloc((size_t)p->k * 2);
+    memcpy(x, act + p->input_offset, (size_t)p->k * 2);
+    for (uint32_t r = 0; r < p->n; r++)
+        q1_store(act, p->output_offset + r, q1_row(weights, p->d_offset, p->qs_offset, p->k, r, x, 0, 1.0f),
+                 p->accumulate);
+    free(x);
+}
+
+void bpo_matvec_q1_0_silu(const bpo_matvec_silu_params* p, const uint8_t* weights, uint16_t* act) {
+    uint16_t* x = (uint16_t*)malloc((size_t)p->k * 2);
+    for (uint32_t i = 0; i < p->k; i++) {                /* matvec_q1_0_silu.wgsl:86-102 */
+        const float g = bpo_f16_to_f32(act[p->gate_offset + i]);
+        const float s = g / (1.0f + expf(-g));
+        x[i] = bpo_f16_mul(bpo_f32_to_f16(s), act[p->up_offset + i]);
+    }
+    for (uint32_t r = 0; r < p->n; r++)
+        q1_store(act, p->output_offset + r, q1_row(weights, p->d_offset, p->qs_offset, p->k, r, x, 0, 1.0f),
+                 p->accumulate);
+    free(x);
+}
+
+void bpo_matvec_q1_0_fused_normed(const bpo_matvec_fused_normed_params* p, const uint8_t* weights,
+                                  uint16_t* act, const uint16_t* w_norms) {
+    const uint32_t k = p->k;
+    uint16_t* x = (uint16_t*)malloc((size_t)k * 2);
+    float thr[256];
+    for (int t = 0; t < 256; t++) thr[t] = 0.0f;
+    for (uint32_t v = 0; v < k / 8; v++)                 /* thread v mod 256 */
+        for (int i = 0; i < 8; i++) {
+            const uint32_t e = 8 * v + i;
+            const uint16_t xh = act[p->input_offset + e];
+            const float xf = bpo_f16_to_f32(xh);
+            thr[v % 256] = thr[v % 256] + xf * xf;
+            x[e] = bpo_f16_mul(xh, w_norms[p->w_norm_off + e]);   /* :102-121 */
+        }
+    float total = 0.0f;
+    for (int w = 0; w < 4; w++) {                        /* each wave: xor butterfly 32 .. 1 */
+        float v[64], nv[64];
+        for (int l = 0; l < 64; l++) v[l] = thr[64 * w + l];
+        for (int off = 32; off >= 1; off >>= 1) {
+            for (int l = 0; l < 64; l++) nv[l] = v[l] + v[l ^ off];
+            memcpy(v, nv, sizeof v);
+        }
+        total = total + v[0];
+    }
+    const float inv_rms = 1.0f / sqrtf(total / (float)k + p->eps);
+    for (uint32_t g = 0; g < p->n_ranges; g++)
+        for (uint32_t r = 0; r < p->n[g]; r++)
+            q1_store(act, p->output_offset[g] + r,
+                     q1_row(weights, p->d_offset[g], p->qs_offset[g], k, r, x, 1, inv_rms), 0);
+    free(x);
+}
+
 static uint64_t splitmix64(uint64_t* s) {
     uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;

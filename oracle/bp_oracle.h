@@ -106,6 +106,34 @@ void bpo_attention(const bpo_attn_params* p, const uint16_t* act, const uint8_t*
                    const uint8_t* kv_v, const uint32_t* tokens, uint32_t n_tokens,
                    uint16_t* act_out, float* out_f32);
 
+/* ---- Q1_0 decode matvecs: src/shaders/matvec_q1_0.wgsl, matvec_q1_0_silu.wgsl,
+ *      matvec_q1_0_fused_normed.wgsl; host src/forward.rs:212-334 ----------- */
+/* f16 add / multiply of two f16 values, rounded once (RNE, subnormals kept). */
+uint16_t bpo_f16_add(uint16_t a, uint16_t b);
+uint16_t bpo_f16_mul(uint16_t a, uint16_t b);
+
+typedef struct {            /* MatvecParams, src/model.rs:105-114 (no dispatch_x_dim) */
+    uint32_t k, n, d_offset, qs_offset, input_offset, output_offset, accumulate;
+} bpo_matvec_params;
+typedef struct {            /* MatvecSiluParams, src/model.rs:117-127 */
+    uint32_t k, n, d_offset, qs_offset, gate_offset, up_offset, output_offset, accumulate;
+} bpo_matvec_silu_params;
+typedef struct {            /* MatvecFusedNormedParams, src/model.rs:150-169 */
+    uint32_t k, input_offset, w_norm_off;
+    float eps;
+    uint32_t n_ranges;
+    uint32_t d_offset[3], qs_offset[3], n[3], output_offset[3];
+} bpo_matvec_fused_normed_params;
+
+/* In place on act (f16 bits); `weights` is the weight buffer (byte offsets). */
+void bpo_matvec_q1_0(const bpo_matvec_params* p, const uint8_t* weights, uint16_t* act);
+void bpo_matvec_q1_0_silu(const bpo_matvec_silu_params* p, const uint8_t* weights, uint16_t* act);
+/* The sum of squares is taken in the GPU kernel's fixed order (256 threads,
+ * 8-element groups, wave butterflies, 4 waves in order); the reference's
+ * subgroupAdd order is backend-defined. */
+void bpo_matvec_q1_0_fused_normed(const bpo_matvec_fused_normed_params* p, const uint8_t* weights,
+                                  uint16_t* act, const uint16_t* w_norms);
+
 /* ---- seeded synthetic inputs (splitmix64 + Box-Muller) -------------------- */
 void bpo_fill_normal_f16(uint64_t seed, float mean, float stddev, uint16_t* out, size_t n);
 

@@ -57,6 +57,25 @@ class AttnParams(ctypes.Structure):
                [("scale", _f32), ("m_tokens", _u32), ("is_prefill", _u32)]
 
 
+class MatvecParams(ctypes.Structure):
+    """MatvecParams, src/model.rs:105-114 (without dispatch_x_dim)."""
+    _fields_ = [(n, _u32) for n in ("k", "n", "d_offset", "qs_offset", "input_offset",
+                                     "output_offset", "accumulate")]
+
+
+class MatvecSiluParams(ctypes.Structure):
+    """MatvecSiluParams, src/model.rs:117-127 (without dispatch_x_dim)."""
+    _fields_ = [(n, _u32) for n in ("k", "n", "d_offset", "qs_offset", "gate_offset", "up_offset",
+                                     "output_offset", "accumulate")]
+
+
+class MatvecFusedNormedParams(ctypes.Structure):
+    """MatvecFusedNormedParams, src/model.rs:150-169, ranges as arrays."""
+    _fields_ = [("k", _u32), ("input_offset", _u32), ("w_norm_off", _u32), ("eps", _f32),
+                ("n_ranges", _u32), ("d_offset", _u32 * 3), ("qs_offset", _u32 * 3), ("n", _u32 * 3),
+                ("output_offset", _u32 * 3)]
+
+
 def _sig(name, res, args):
     f = getattr(_lib, name)
     f.restype, f.argtypes = res, args
@@ -85,6 +104,12 @@ _split = _sig("bpo_attention_split_merge", None, [ctypes.POINTER(AttnSplitParams
 _attn = _sig("bpo_attention", None, [ctypes.POINTER(AttnParams), _vp, _vp, _vp, _vp, _u32, _vp,
                                     _vp])
 _fill = _sig("bpo_fill_normal_f16", None, [_u64, _f32, _f32, _vp, ctypes.c_size_t])
+_f16_add = _sig("bpo_f16_add", ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16])
+_f16_mul = _sig("bpo_f16_mul", ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16])
+_mv = _sig("bpo_matvec_q1_0", None, [ctypes.POINTER(MatvecParams), _vp, _vp])
+_mv_silu = _sig("bpo_matvec_q1_0_silu", None, [ctypes.POINTER(MatvecSiluParams), _vp, _vp])
+_mv_normed = _sig("bpo_matvec_q1_0_fused_normed", None, [ctypes.POINTER(MatvecFusedNormedParams), _vp,
+                                                         _vp, _vp])
 
 
 def _ptr(a):
@@ -204,3 +229,46 @@ def fill_normal_f16(seed: int, n: int, mean=0.0, std=1.0) -> np.ndarray:
     out = np.empty(n, np.uint16)
     _fill(seed, mean, std, _ptr(out), n)
     return out
+
+
+# ---- Q1_0 matvecs (matvec_q1_0*.wgsl) -----------------------------------------
+def f16_add(a: int, b: int) -> int:
+    return int(_f16_add(a, b))
+
+
+def f16_mul(a: int, b: int) -> int:
+    return int(_f16_mul(a, b))
+
+
+def matvec_q1_0(p: MatvecParams, weights: np.ndarray, act) -> np.ndarray:
+    """Returns a copy of act (uint16) with the output rows written."""
+    out = _u16(act).copy()
+    _mv(ctypes.byref(p), _ptr(np.ascontiguousarray(weights, np.uint8)), _ptr(out))
+    return out
+
+
+def matvec_q1_0_silu(p: MatvecSiluParams, weights: np.ndarray, act) -> np.ndarray:
+    out = _u16(act).copy()
+    _mv_silu(ctypes.byref(p), _ptr(np.ascontiguousarray(weights, np.uint8)), _ptr(out))
+    return out
+
+
+def matvec_q1_0_fused_normed(p: MatvecFusedNormedParams, weights: np.ndarray, act, w_norms) -> np.ndarray:
+    out = _u16(act).copy()
+    _mv_normed(ctypes.byref(p), _ptr(np.ascontiguousarray(weights, np.uint8)), _ptr(out),
+               _ptr(_u16(w_norms)))
+    return out
+
+
+def q1_0_tensor(rng: np.random.Generator, n: int, k: int, d_scale=0.02):
+    """Random Q1_0 tensor (d f16 then qs, the model.rs:784-804 layout) as bytes,
+    with the d / qs byte offsets relative to its start."""
+    nb = k // 128
+    d = (rng.standard_normal(n * nb) * d_scale).astype(np.float16)
+    qs = rng.integers(0, 256, size=n * nb * 16, dtype=np.uint8)
+    d_bytes = d.view(np.uint8)
+    qs_off = (d_bytes.size + 3) // 4 * 4
+    buf = np.zeros(qs_off + qs.size, np.uint8)
+    buf[:d_bytes.size] = d_bytes
+    buf[qs_off:] = qs
+    return buf, 0, qs_off

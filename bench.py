@@ -12,7 +12,9 @@ value = algorithmic bytes per step / step time, with per layer
 
 Also reported: decode at ctx 32768 (config 5, rotating over 8 layers),
 prefill pp2048 (metric) and the 2048-on-2048 chunked prefill (config 4) in
-TFLOP/s of unmasked QK^T + PV work, and the CPU oracle on a bounded sample.
+TFLOP/s of unmasked QK^T + PV work, the Bonsai-4B per-layer Q1_0 decode
+matvecs (fused normed q/k/v, o, fused normed gate/up, silu down) over 36
+layers of distinct weights in GB/s, and the CPU oracle on a bounded sample.
 """
 import argparse
 import json
@@ -46,7 +48,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "prefill", "chunked", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "prefill", "chunked", "matvec", "copy"], default=None,
                     help="run only one workload (for profiling)")
     return ap.parse_args()
 
@@ -231,6 +233,100 @@ def bench_copy(torch, args, nbytes=1 << 30):
             "GBps_read_plus_write": 2 * nbytes / (us * 1e-6) / 1e9}
 
 
+Q1_BYTES_PER_WEIGHT = 1 / 8 + 2 / 128     # Q1_0: 1 bit + one f16 scale per 128 weights
+
+
+class MatvecLayers:
+    """Bonsai-4B matvec weights of n_layer layers, each layer one byte buffer
+    [qkv d | qkv qs | o d | o qs | gate/up d | gate/up qs | down d | down qs]
+    (random signs, N(0, 0.02) f16 scales), plus an f16 activation buffer
+    x [2560] | q [4096] | k [1024] | v [1024] | attn_out [4096] | gate [9728] |
+    up [9728] | h [2560]."""
+    HIDDEN, Q_DIM, KV_DIM, FFN = 2560, 4096, 1024, 9728
+
+    def __init__(self, torch, n_layer, seed=0):
+        from bonsai_pot_amd import Model, layout
+        self.model = Model(layout.Config(n_layer=1), 64)
+        self.model.set_stream(torch.cuda.current_stream().cuda_stream)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        H, Q, KV, F = self.HIDDEN, self.Q_DIM, self.KV_DIM, self.FFN
+        self.tensors = {"qkv": (Q + 2 * KV, H), "o": (H, Q), "gate_up": (2 * F, H), "down": (H, F)}
+        self.offs, at = {}, 0
+        for name, (n, k) in self.tensors.items():
+            nb = k // 128
+            d_off = at
+            qs_off = (d_off + 2 * n * nb + 255) // 256 * 256
+            at = (qs_off + 16 * n * nb + 255) // 256 * 256
+            self.offs[name] = (d_off, qs_off)
+        self.layer_bytes = at
+        self.bufs = []
+        for _ in range(n_layer):
+            buf = torch.randint(-128, 128, (at,), generator=g, device="cuda", dtype=torch.int8)
+            for name, (n, k) in self.tensors.items():
+                d_off, _ = self.offs[name]
+                nd = n * (k // 128)
+                d = (torch.randn(nd, generator=g, device="cuda") * 0.02).to(torch.float16)
+                buf[d_off:d_off + 2 * nd].copy_(d.view(torch.int8))
+            self.bufs.append(buf)
+        self.x, self.q = 0, H
+        self.k, self.v = H + Q, H + Q + KV
+        self.attn, self.gate = H + Q + 2 * KV, H + 2 * Q + 2 * KV
+        self.up, self.h = self.gate + F, self.gate + 2 * F
+        self.act = torch.randn(self.h + H, generator=g, device="cuda").to(torch.float16)
+        self.wn = (1 + 0.1 * torch.randn(2 * H, generator=g, device="cuda")).to(torch.float16)
+
+    def weight_bytes(self, name):
+        n, k = self.tensors[name]
+        return int(n * k * Q1_BYTES_PER_WEIGHT)
+
+    def launch(self, name, il):
+        """One matvec of layer il, as the reference's decode layer issues it."""
+        m, w, a, H = self.model, self.bufs[il].data_ptr(), self.act.data_ptr(), self.HIDDEN
+        d_off, qs_off = self.offs[name]
+        if name == "qkv":
+            nb = H // 128
+            Q, KV = self.Q_DIM, self.KV_DIM
+            rng = [(d_off, qs_off, Q, self.q),
+                   (d_off + 2 * Q * nb, qs_off + 16 * Q * nb, KV, self.k),
+                   (d_off + 2 * (Q + KV) * nb, qs_off + 16 * (Q + KV) * nb, KV, self.v)]
+            m.dispatch_matvec_q1_0_fused_normed(w, a, self.wn.data_ptr(), H, self.x, 0, rng)
+        elif name == "o":
+            m.dispatch_matvec_q1_0(w, a, self.Q_DIM, H, d_off, qs_off, self.attn, self.x, True)
+        elif name == "gate_up":
+            F, nb = self.FFN, H // 128
+            rng = [(d_off, qs_off, F, self.gate), (d_off + 2 * F * nb, qs_off + 16 * F * nb, F, self.up)]
+            m.dispatch_matvec_q1_0_fused_normed(w, a, self.wn.data_ptr(), H, self.x, H, rng)
+        else:
+            m.dispatch_matvec_q1_0_silu(w, a, self.FFN, H, d_off, qs_off, self.gate, self.up, self.x, True)
+
+
+def bench_matvec(torch, args, n_layer=36):
+    """The four Q1_0 matvec dispatches of a Bonsai-4B decode layer, over 36
+    layers of distinct weights (520 MB, above the 256 MB Infinity Cache) so
+    each launch streams its weights from HBM. Bytes = weights (1/8 + 2/128 B
+    per weight) + f16 activations in and out."""
+    b = MatvecLayers(torch, n_layer)
+    names = list(b.tensors)
+    for il in range(2):
+        for nm in names:
+            b.launch(nm, il)
+    torch.cuda.synchronize()
+    act_bytes = {"qkv": 2 * (2 * b.HIDDEN + 2 * b.HIDDEN) + 2 * 6144, "o": 2 * (b.Q_DIM + 2 * b.HIDDEN),
+                 "gate_up": 2 * (2 * b.HIDDEN) + 2 * 2 * b.FFN, "down": 2 * (2 * b.FFN + 2 * b.HIDDEN)}
+    res = {"layers": n_layer, "layer_weight_bytes": sum(b.weight_bytes(n) for n in names)}
+    g = make_graph(torch, b, lambda: [b.launch(nm, il) for il in range(n_layer) for nm in names])
+    step_s = time_region(torch, g.replay, max(5, args.steps // 5), 2)
+    step_bytes = n_layer * sum(b.weight_bytes(n) + act_bytes[n] for n in names)
+    res.update({"ms_per_step_36_layers": step_s * 1e3, "step_GBps": step_bytes / step_s / 1e9})
+    for nm in names:
+        us = per_launch_us(torch, b, lambda i, nm=nm: b.launch(nm, i % n_layer), n_layer)
+        byt = b.weight_bytes(nm) + act_bytes[nm]
+        res[nm] = {"n_k": b.tensors[nm], "kernel_us_avg": us, "bytes": byt,
+                   "GBps": byt / (us * 1e-6) / 1e9, "frac_hbm": byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    b.model.close()
+    return res
+
+
 def measured_traffic(workload, kernel):
     """HBM bytes per dispatch of `kernel` in `workload`, measured with rocprofv3
     FETCH_SIZE / WRITE_SIZE (scaled by a copy kernel of known size), from
@@ -317,6 +413,8 @@ def main():
         extras["prefill_pp512"] = bench_prefill(torch, args, 512, 0)
     if args.only in (None, "chunked"):
         extras["chunked_prefill_2048_on_2048"] = bench_prefill(torch, args, 2048, 2048)
+    if args.only in (None, "matvec"):
+        extras["matvec_q1_0_4b_layer"] = bench_matvec(torch, args)
     if args.only == "copy":
         extras["copy_1GiB"] = bench_copy(torch, args)
     if args.only is not None:

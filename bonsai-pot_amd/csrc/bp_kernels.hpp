@@ -113,6 +113,7 @@ struct MatvecArgs {
     float eps;
     uint32_t accumulate;      // plain / silu: y = f16(f32(y) + acc)
     MatvecRange range[3];     // plain / silu: range[0] only; normed: multiples of 32 rows
+    uint32_t rows_per_wg;     // set by launch_matvec_q1_0 (8 or 16)
 };
 // mode 0: matvec_q1_0, 1: matvec_q1_0_silu, 2: matvec_q1_0_fused_normed.
 hipError_t launch_matvec_q1_0(const MatvecArgs& a, int mode, hipStream_t s);

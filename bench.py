@@ -324,7 +324,42 @@ def bench_matvec(torch, args, n_layer=36):
         res[nm] = {"n_k": b.tensors[nm], "kernel_us_avg": us, "bytes": byt,
                    "GBps": byt / (us * 1e-6) / 1e9, "frac_hbm": byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
     b.model.close()
+    res["lm_head"] = bench_lm_head(torch, args)
     return res
+
+
+def bench_lm_head(torch, args, vocab=151936, n_copies=8):
+    """The LM head matvec (vocab x 2560 Q1_0, 54.7 MB) over 8 copies of the
+    weights (438 MB, above the Infinity Cache)."""
+    from bonsai_pot_amd import Model, layout
+    H = MatvecLayers.HIDDEN
+    nb = H // 128
+    m = Model(layout.Config(n_layer=1), 64)
+    m.set_stream(torch.cuda.current_stream().cuda_stream)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    d_bytes = 2 * vocab * nb
+    qs_off = (d_bytes + 255) // 256 * 256
+    size = qs_off + 16 * vocab * nb
+    bufs = []
+    for _ in range(n_copies):
+        buf = torch.randint(-128, 128, (size,), generator=g, device="cuda", dtype=torch.int8)
+        d = (torch.randn(vocab * nb, generator=g, device="cuda") * 0.02).to(torch.float16)
+        buf[:d_bytes].copy_(d.view(torch.int8))
+        bufs.append(buf)
+    act = torch.randn(H + vocab, generator=g, device="cuda").to(torch.float16)
+
+    class _B:
+        model = m
+    launch = lambda i: m.dispatch_matvec_q1_0(bufs[i % n_copies].data_ptr(), act.data_ptr(), H, vocab, 0, qs_off,
+                                              0, H, False)
+    for i in range(n_copies):
+        launch(i)
+    torch.cuda.synchronize()
+    us = per_launch_us(torch, _B, launch, 2 * n_copies)
+    byt = int(vocab * H * Q1_BYTES_PER_WEIGHT) + 2 * (H + vocab)
+    m.close()
+    return {"n_k": [vocab, H], "kernel_us_avg": us, "bytes": byt, "GBps": byt / (us * 1e-6) / 1e9,
+            "frac_hbm": byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
 def measured_traffic(workload, kernel):

@@ -42,6 +42,8 @@ struct bp_model {
     uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
+    int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 f16 sums in the reference's order, 2 i8 MFMA
+    uint32_t matvec_stream_min_tiles;
     bool lost;
     std::string lost_message;
 };
@@ -248,6 +250,21 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
     if (const char* env = std::getenv("BP_DECODE_WIDE_MIN_ROWS")) {
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 0) m->decode_wide_min_rows = static_cast<uint32_t>(v);
+    }
+    // Q1_0 matvec arithmetic: "f16" = the reference's f16 sums, bit for bit
+    // (VALU-bound); "mfma" = exact integer sums of 15-bit x on the i8 matrix
+    // cores; default "auto" = f16 below the streaming size, MFMA from it on
+    // (the LM head), where the f16 kernel's VALU work exceeds its HBM time.
+    m->matvec_arith = 0;
+    if (const char* env = std::getenv("BP_MATVEC_ARITH")) {
+        if (std::strcmp(env, "f16") == 0) m->matvec_arith = 1;
+        else if (std::strcmp(env, "mfma") == 0) m->matvec_arith = 2;
+    }
+    // MFMA matvec: 16-row tiles from which each wave streams whole tiles.
+    m->matvec_stream_min_tiles = 2048;
+    if (const char* env = std::getenv("BP_MATVEC_STREAM_MIN_TILES")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 1) m->matvec_stream_min_tiles = static_cast<uint32_t>(v);
     }
     m->partials_floats = static_cast<uint64_t>(cfg->n_head) * bp::decode_max_splits() *
                          bp::decode_partial_stride();
@@ -482,6 +499,8 @@ static bp_status matvec_common(bp_model* m, const void* weights, void* act, uint
     a.act = static_cast<uint16_t*>(act);
     a.k = k;
     a.eps = m->cfg.rms_eps;
+    a.stream_min_tiles = m->matvec_stream_min_tiles;
+    a.cu_count = static_cast<uint32_t>(m->cu_count);
     return BP_OK;
 }
 
@@ -489,6 +508,12 @@ static bp_status matvec_check_tensor(uint32_t w_d, uint32_t w_qs) {
     if ((w_d & 1u) || (w_qs & 3u))
         return fail(BP_ERR_INVALID_ARG, "Q1_0 offsets: d must be 2-byte, qs 4-byte aligned (%u, %u)", w_d, w_qs);
     return BP_OK;
+}
+
+static hipError_t launch_matvec(const bp_model* m, const bp::MatvecArgs& a, int mode) {
+    const bool mfma = m->matvec_arith == 2 ||
+                      (m->matvec_arith == 0 && (a.n_total + 15) / 16 >= m->matvec_stream_min_tiles);
+    return mfma ? bp::launch_matvec_q1_0_mfma(a, mode, m->stream) : bp::launch_matvec_q1_0(a, mode, m->stream);
 }
 
 bp_status bp_dispatch_matvec_q1_0(bp_model* m, const void* weights, void* act, uint32_t k, uint32_t n,
@@ -504,7 +529,7 @@ bp_status bp_dispatch_matvec_q1_0(bp_model* m, const void* weights, void* act, u
     a.input_offset = in_off;
     a.accumulate = accumulate ? 1u : 0u;
     a.range[0] = {w_d, w_qs, n, out_off};
-    return hip_check(m, bp::launch_matvec_q1_0(a, 0, m->stream), "matvec_q1_0 launch");
+    return hip_check(m, launch_matvec(m, a, 0), "matvec_q1_0 launch");
 }
 
 bp_status bp_dispatch_matvec_q1_0_silu(bp_model* m, const void* weights, void* act, uint32_t k, uint32_t n,
@@ -522,7 +547,7 @@ bp_status bp_dispatch_matvec_q1_0_silu(bp_model* m, const void* weights, void* a
     a.up_offset = up_off;
     a.accumulate = accumulate ? 1u : 0u;
     a.range[0] = {w_d, w_qs, n, out_off};
-    return hip_check(m, bp::launch_matvec_q1_0(a, 1, m->stream), "matvec_q1_0_silu launch");
+    return hip_check(m, launch_matvec(m, a, 1), "matvec_q1_0_silu launch");
 }
 
 bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* m, const void* weights, void* act, const void* w_norms,
@@ -548,7 +573,7 @@ bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* m, const void* weights,
     a.n_total = static_cast<uint32_t>(total);
     a.input_offset = in_off;
     a.w_norm_off = w_norm_off;
-    return hip_check(m, bp::launch_matvec_q1_0(a, 2, m->stream), "matvec_q1_0_fused_normed launch");
+    return hip_check(m, launch_matvec(m, a, 2), "matvec_q1_0_fused_normed launch");
 }
 
 static bp_status snapshot_copy(bp_model* m, uint32_t pos, uint8_t* payload, uint64_t payload_bytes,

@@ -113,10 +113,13 @@ struct MatvecArgs {
     float eps;
     uint32_t accumulate;      // plain / silu: y = f16(f32(y) + acc)
     MatvecRange range[3];     // plain / silu: range[0] only; normed: multiples of 32 rows
-    uint32_t rows_per_wg;     // set by launch_matvec_q1_0 (8 or 16)
+    uint32_t rows_per_wg;     // set by the launchers
+    uint32_t stream_min_tiles;   // MFMA matvec: rows / 16 from which waves stream whole tiles
+    uint32_t cu_count;
 };
 // mode 0: matvec_q1_0, 1: matvec_q1_0_silu, 2: matvec_q1_0_fused_normed.
 hipError_t launch_matvec_q1_0(const MatvecArgs& a, int mode, hipStream_t s);
+hipError_t launch_matvec_q1_0_mfma(const MatvecArgs& a, int mode, hipStream_t s);
 uint32_t matvec_max_k();
 
 hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t m_tokens,

@@ -187,6 +187,17 @@ def test_oracle_silu_and_normed_vs_f64():
 
 
 # ---------------------------------------------------------------- GPU: HIP vs oracle
+# Two arithmetics (BP_MATVEC_ARITH, read at model creation):
+#  * "f16": the reference's f16 sums in its order -> bit-exact with the oracle;
+#  * "mfma" (default): x rounded to 15 bits of each block's max |x|, exact
+#    integer sums, f32 scaling -> within the bound of _mfma_bound of the exact
+#    f64 product of the staged x, and within that bound plus the oracle's own
+#    f16-accumulation bound of the oracle. "mfma_stream" forces the MFMA
+#    kernel's streaming schedule (each wave walks whole 16-row tiles), which it
+#    otherwise takes from 2048 tiles on (BP_MATVEC_STREAM_MIN_TILES).
+ARITHS = ["f16", "mfma", "mfma_stream"]
+
+
 def _dev(arr):
     import torch
     return torch.from_numpy(np.ascontiguousarray(arr).view(np.int8 if arr.dtype == np.uint8 else np.int16)).cuda()
@@ -198,19 +209,55 @@ def _host(t):
     return t.cpu().numpy().view(np.uint16)
 
 
-def _model():
+def _model(monkeypatch, arith):
     import torch
     from bonsai_pot_amd import Model, layout
+    monkeypatch.setenv("BP_MATVEC_ARITH", "mfma" if arith.startswith("mfma") else arith)
+    monkeypatch.setenv("BP_MATVEC_STREAM_MIN_TILES", "1" if arith == "mfma_stream" else "2048")
     m = Model(layout.Config(n_layer=1), 64)
     m.set_stream(torch.cuda.current_stream().cuda_stream)
     return m
 
 
+def _mfma_bound(buf, d_off, qs_off, n, k, x, scale=1.0):
+    """Bound on |mfma result - exact| before the f16 store: each x moves by at
+    most half of its block's quantum max|x| / 16383, and f32 terms and sums by
+    a few ulps."""
+    d, _ = _decode(buf, d_off, qs_off, n, k)
+    xb = np.abs(x).reshape(k // 128, 128)
+    quant = 128 * xb.max(-1) / 32766 * 1.001
+    f32 = 8 * 2.0**-24 * xb.sum(-1)
+    return scale * (np.abs(d) * (quant + f32)[None, :]).sum(-1)
+
+
+def _check(arith, got, want_oracle, out, n, exact, bound_mfma, bound_oracle, old=None, written=None):
+    """got / want_oracle: whole act buffers (uint16); exact / bounds per row;
+    written: every (offset, rows) output region of the call (default this one)."""
+    if arith == "f16":
+        bad = np.flatnonzero(got != want_oracle)
+        assert bad.size == 0, f"{bad.size} f16 outputs differ, first at {bad[:8]}"
+        return
+    mask = np.ones(got.size, bool)
+    for o_, n_ in (written or [(out, n)]):
+        mask[o_:o_ + n_] = False
+    assert np.array_equal(got[mask], want_oracle[mask]), "matvec wrote outside its output rows"
+    y = got[out:out + n].view(np.float16).astype(np.float64)
+    ref = exact if old is None else exact + old
+    tol = bound_mfma + 2.0**-11 * np.abs(ref) + 2.0**-24
+    err = np.abs(y - ref)
+    assert np.all(err <= tol), f"vs exact: worst row {np.argmax(err - tol)}, excess {(err - tol).max():.3g}"
+    yo = want_oracle[out:out + n].view(np.float16).astype(np.float64)
+    tol2 = tol + bound_oracle + 2.0**-11 * np.abs(yo)
+    assert np.all(np.abs(y - yo) <= tol2), "vs oracle outside the two bounds"
+    _say(f"  max |gpu - exact| / bound = {(err / tol).max():.3f}; max |gpu - oracle| = {np.abs(y - yo).max():.3g}")
+
+
 @pytest.mark.gpu
+@pytest.mark.parametrize("arith", ARITHS)
 @pytest.mark.parametrize("n,k,acc", [(Q_DIM, HIDDEN, 0), (HIDDEN, Q_DIM, 1), (KV_DIM, HIDDEN, 0),
-                                     (37, 128, 0), (1, 16384, 1), (HIDDEN, FFN, 0)])
-def test_matvec_bit_exact(cuda, n, k, acc):
-    _say(f"[matvec] n={n} k={k} acc={acc}")
+                                     (37, 128, 0), (1, 16384, 1), (HIDDEN, FFN, 0), (70, 2432, 0)])
+def test_matvec(cuda, monkeypatch, arith, n, k, acc):
+    _say(f"[matvec] {arith} n={n} k={k} acc={acc}")
     rng = np.random.default_rng(n + k)
     buf, [(d_off, qs_off)] = _weights(rng, [(n, k)])
     in_off, out_off = 8, 8 + k + 24
@@ -219,17 +266,21 @@ def test_matvec_bit_exact(cuda, n, k, acc):
                          output_offset=out_off, accumulate=acc)
     want = orc.matvec_q1_0(p, buf, act)
     w_d, a_d = _dev(buf), _dev(act)
-    m = _model()
+    m = _model(monkeypatch, arith)
     m.dispatch_matvec_q1_0(w_d.data_ptr(), a_d.data_ptr(), k, n, d_off, qs_off, in_off, out_off, bool(acc))
     got = _host(a_d)
-    bad = np.flatnonzero(got != want)
-    assert bad.size == 0, f"{bad.size} f16 outputs differ, first at {bad[:8]}"
+    x = act[in_off:in_off + k].view(np.float16).astype(np.float64)
+    exact, _ = _brute(buf, d_off, qs_off, n, k, x)
+    old = act[out_off:out_off + n].view(np.float16).astype(np.float64) if acc else None
+    _check(arith, got, want, out_off, n, exact, _mfma_bound(buf, d_off, qs_off, n, k, x),
+           _f16_sum_bound(buf, d_off, qs_off, n, k, x), old)
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("arith", ARITHS)
 @pytest.mark.parametrize("n,k,acc", [(HIDDEN, FFN, 1), (HIDDEN, FFN, 0), (64, 1024, 0)])
-def test_matvec_silu(cuda, n, k, acc):
-    _say(f"[matvec_silu] n={n} k={k} acc={acc}")
+def test_matvec_silu(cuda, monkeypatch, arith, n, k, acc):
+    _say(f"[matvec_silu] {arith} n={n} k={k} acc={acc}")
     rng = np.random.default_rng(7 * n + k)
     buf, [(d_off, qs_off)] = _weights(rng, [(n, k)])
     gate_off, up_off, out_off = 0, k + 16, 2 * k + 32
@@ -238,44 +289,53 @@ def test_matvec_silu(cuda, n, k, acc):
                              up_offset=up_off, output_offset=out_off, accumulate=acc)
     want = orc.matvec_q1_0_silu(p, buf, act)
     w_d, a_d = _dev(buf), _dev(act)
-    m = _model()
+    m = _model(monkeypatch, arith)
     m.dispatch_matvec_q1_0_silu(w_d.data_ptr(), a_d.data_ptr(), k, n, d_off, qs_off, gate_off, up_off,
                                 out_off, bool(acc))
     got = _host(a_d)
     assert np.array_equal(got[:out_off], act[:out_off])
-    g = got[out_off:].view(np.float16).astype(np.float64)
-    w = want[out_off:].view(np.float16).astype(np.float64)
-    # an ulp of difference in silu(g) changes one f16 x; bound the row effect by
-    # 2^-10 of the row's |d| . |x| plus one output ulp
-    _, mag = _brute(buf, d_off, qs_off, n, k, np.abs(act[up_off:up_off + k].view(np.float16)).astype(np.float64) * 4)
-    exact = np.mean(got[out_off:] == want[out_off:])
-    _say(f"  bit-identical rows: {exact:.4f}")
-    assert np.all(np.abs(g - w) <= 2.0**-10 * mag + 2.0**-10 * np.abs(w) + 1e-6)
-    assert exact > 0.9
+    # staged x as the oracle forms it (libm expf; the device expf may differ by
+    # an ulp, which can move one f16 x by one ulp: 2^-10 |x| per element)
+    g = act[gate_off:gate_off + k].view(np.float16).astype(np.float32)
+    u = act[up_off:up_off + k].view(np.float16)
+    x = ((g / (np.float32(1) + np.exp(-g))).astype(np.float16) * u).astype(np.float64)
+    exact, _ = _brute(buf, d_off, qs_off, n, k, x)
+    d, _ = _decode(buf, d_off, qs_off, n, k)
+    ulp_x = (np.abs(d) * (2.0**-10 * np.abs(x)).reshape(k // 128, 128).sum(-1)[None, :]).sum(-1)
+    old = act[out_off:out_off + n].view(np.float16).astype(np.float64) if acc else None
+    if arith == "f16":
+        gg = got[out_off:].view(np.float16).astype(np.float64)
+        ww = want[out_off:].view(np.float16).astype(np.float64)
+        assert np.all(np.abs(gg - ww) <= ulp_x + 2.0**-10 * np.abs(ww) + 1e-6)
+        _say(f"  bit-identical rows: {np.mean(got[out_off:] == want[out_off:]):.4f}")
+        return
+    _check(arith, got, want, out_off, n, exact, _mfma_bound(buf, d_off, qs_off, n, k, x) + ulp_x,
+           _f16_sum_bound(buf, d_off, qs_off, n, k, x), old)
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("arith", ARITHS)
 @pytest.mark.parametrize("ranges", [
     [(Q_DIM, 0), (KV_DIM, 1), (KV_DIM, 2)],          # q / k / v from attn_norm(x)
     [(FFN, 0), (FFN, 1)],                            # gate / up from ffn_norm(x)
     [(96, 0)],
 ])
-def test_matvec_fused_normed_bit_exact(cuda, ranges):
+def test_matvec_fused_normed(cuda, monkeypatch, arith, ranges):
     k = HIDDEN
-    _say(f"[matvec_fused_normed] ranges={ranges}")
+    _say(f"[matvec_fused_normed] {arith} ranges={ranges}")
     rng = np.random.default_rng(len(ranges) * 11 + ranges[0][0])
     buf, offs = _weights(rng, [(n, k) for n, _ in ranges])
     total = sum(n for n, _ in ranges)
-    in_off, w_norm_off = 0, 0
+    in_off = 0
     act = np.concatenate([_f16(rng.standard_normal(k) * 4), np.zeros(total + 8, np.uint16)])
     wn = _f16(1 + 0.2 * rng.standard_normal(k + 16))
     w_norm_off = 16
-    # output regions in a different order from the ranges
-    outs, at = {}, k + 8
+    outs, at = {}, k + 8        # output regions in a different order from the ranges
     for n, tag in sorted(ranges, key=lambda r: -r[1]):
         outs[tag] = at
         at += n
-    eps = 1e-6     # the model's rms_eps
+    from bonsai_pot_amd import layout
+    eps = layout.Config(n_layer=1).rms_eps
     pn = orc.MatvecFusedNormedParams(k=k, input_offset=in_off, w_norm_off=w_norm_off, eps=eps,
                                      n_ranges=len(ranges))
     r_list = []
@@ -283,21 +343,58 @@ def test_matvec_fused_normed_bit_exact(cuda, ranges):
         pn.d_offset[i], pn.qs_offset[i], pn.n[i], pn.output_offset[i] = d_o, q_o, n, outs[tag]
         r_list.append((d_o, q_o, n, outs[tag]))
     want = orc.matvec_q1_0_fused_normed(pn, buf, act, wn)
-    from bonsai_pot_amd import layout
-    assert layout.Config(n_layer=1).rms_eps == eps
     w_d, a_d, n_d = _dev(buf), _dev(act), _dev(wn)
-    m = _model()
+    m = _model(monkeypatch, arith)
     m.dispatch_matvec_q1_0_fused_normed(w_d.data_ptr(), a_d.data_ptr(), n_d.data_ptr(), k, in_off,
                                         w_norm_off, r_list)
     got = _host(a_d)
-    bad = np.flatnonzero(got != want)
-    assert bad.size == 0, f"{bad.size} f16 outputs differ, first at {bad[:8]}"
+    if arith == "f16":
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"{bad.size} f16 outputs differ, first at {bad[:8]}"
+        return
+    xin = act[in_off:in_off + k].view(np.float16)
+    x = (xin * wn[w_norm_off:w_norm_off + k].view(np.float16)).astype(np.float64)
+    inv = 1 / np.sqrt((xin.astype(np.float64) ** 2).mean() + eps)
+    for (n, tag), (d_o, q_o) in zip(ranges, offs):
+        o = outs[tag]
+        exact, _ = _brute(buf, d_o, q_o, n, k, x)
+        mag = _mfma_bound(buf, d_o, q_o, n, k, x, inv) + 1e-5 * np.abs(exact * inv)   # inv_rms in f32
+        _check(arith, got, want, o, n, exact * inv, mag, inv * _f16_sum_bound(buf, d_o, q_o, n, k, x),
+               written=[(outs[tg], nn) for nn, tg in ranges])
 
 
 @pytest.mark.gpu
-def test_matvec_rejects_bad_shapes(cuda):
+@pytest.mark.parametrize("min_tiles,want_exact", [("2048", True), ("1", False)])
+def test_matvec_auto_dispatch(cuda, monkeypatch, min_tiles, want_exact):
+    """Default arithmetic: the f16-order kernel (bit-exact) below the streaming
+    size, the MFMA kernel from it on."""
+    import torch
+    from bonsai_pot_amd import Model, layout
+    monkeypatch.delenv("BP_MATVEC_ARITH", raising=False)
+    monkeypatch.setenv("BP_MATVEC_STREAM_MIN_TILES", min_tiles)
+    n, k = 512, 2560
+    rng = np.random.default_rng(5)
+    buf, [(d_off, qs_off)] = _weights(rng, [(n, k)])
+    act = _f16(rng.standard_normal(k + n))
+    p = orc.MatvecParams(k=k, n=n, d_offset=d_off, qs_offset=qs_off, input_offset=0, output_offset=k,
+                         accumulate=0)
+    want = orc.matvec_q1_0(p, buf, act)
+    m = Model(layout.Config(n_layer=1), 64)
+    m.set_stream(torch.cuda.current_stream().cuda_stream)
+    w_d, a_d = _dev(buf), _dev(act)
+    m.dispatch_matvec_q1_0(w_d.data_ptr(), a_d.data_ptr(), k, n, d_off, qs_off, 0, k, False)
+    got = _host(a_d)
+    assert np.array_equal(got, want) == want_exact
+    x = act[:k].view(np.float16).astype(np.float64)
+    exact, _ = _brute(buf, d_off, qs_off, n, k, x)
+    _check("mfma", got, want, k, n, exact, _mfma_bound(buf, d_off, qs_off, n, k, x),
+           _f16_sum_bound(buf, d_off, qs_off, n, k, x))
+
+
+@pytest.mark.gpu
+def test_matvec_rejects_bad_shapes(cuda, monkeypatch):
     from bonsai_pot_amd.errors import PotError
-    m = _model()
+    m = _model(monkeypatch, "mfma")
     import torch
     w = torch.zeros(1 << 16, dtype=torch.int8, device="cuda")
     a = torch.zeros(1 << 16, dtype=torch.int16, device="cuda")

@@ -562,8 +562,8 @@ bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* m, const void* weights,
         return fail(BP_ERR_INVALID_ARG, "matvec in_off / w_norm_off (%u, %u) must be multiples of 8", in_off, w_norm_off);
     uint64_t total = 0;
     for (uint32_t i = 0; i < n_ranges; i++) {
-        if (ranges[i].n % 32 != 0)
-            return fail(BP_ERR_INVALID_ARG, "fused normed matvec range %u: n = %u not a multiple of 32", i, ranges[i].n);
+        if (ranges[i].n % 16 != 0)
+            return fail(BP_ERR_INVALID_ARG, "fused normed matvec range %u: n = %u not a multiple of 16", i, ranges[i].n);
         if ((st = matvec_check_tensor(ranges[i].d_offset, ranges[i].qs_offset)) != BP_OK) return st;
         a.range[i] = {ranges[i].d_offset, ranges[i].qs_offset, ranges[i].n, ranges[i].output_offset};
         total += ranges[i].n;

@@ -128,8 +128,8 @@ __global__ __launch_bounds__(kMvMaxThreads) void matvec_q1_0_kernel(MatvecArgs a
     const uint32_t rows = a.rows_per_wg;
     float* terms = reinterpret_cast<float*>(x_sh + nb * kBlockHalves);   // [rows][nb]
 
-    // This workgroup's rows lie in one range (ranges are multiples of 32 rows
-    // and rows_per_wg divides 32).
+    // This workgroup's rows lie in one range (ranges are multiples of 16 rows
+    // and rows_per_wg divides 16).
     const uint32_t row0 = blockIdx.x * rows;
     uint32_t d_off = a.range[0].d_offset, qs_off = a.range[0].qs_offset, out_off = a.range[0].output_offset;
     uint32_t rbase = row0;                       // first row of the workgroup within its range

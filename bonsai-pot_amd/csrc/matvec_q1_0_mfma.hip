@@ -62,7 +62,7 @@ __host__ __device__ inline MfLayout mf_layout(uint32_t nb, uint32_t n_groups, ui
 }
 
 // Rows of one 16-row tile (global tile index T: rows 16T .. 16T + 15 over
-// all ranges; ranges are multiples of 32 rows, so a tile lies in one range).
+// all ranges; ranges are multiples of 16 rows, so a tile lies in one range).
 struct TileRows {
     uint32_t rbase;    // first row of the tile within its range
     uint32_t n_here;   // rows of the tile that exist (0..16)
@@ -398,7 +398,12 @@ hipError_t launch_matvec_q1_0_mfma(const MatvecArgs& args, int mode, hipStream_t
         if (n_wg > 4 * a.cu_count) n_wg = 4 * a.cu_count;   // all resident at once
         a.rows_per_wg = 0;
     } else {
-        a.rows_per_wg = 2 * n_groups <= 16 ? 32 : 16;
+        // (a workgroup's rows must lie in one range: ranges of the normed matvec
+        // are multiples of 16 rows, 32 allows two tiles)
+        bool ranges32 = true;
+        if (mode == 2)
+            for (int i = 0; i < 3; i++) ranges32 = ranges32 && a.range[i].n % 32 == 0;
+        a.rows_per_wg = 2 * n_groups <= 16 && ranges32 ? 32 : 16;
         tiles = a.rows_per_wg / 16;
         waves = tiles * n_groups;
         if (waves > 16) waves = 16;

@@ -146,7 +146,10 @@ bp_status bp_dispatch_attention(bp_model* model, void* act, uint32_t q_off, uint
  * src/model.rs:784-804). k is a multiple of 128, at most 16384; activation
  * offsets are f16-element offsets into `act` and must be multiples of 8.
  * y[out_off + r] = f16(sum_b d[r][b] * sum_e (+-x[e])) (or, with accumulate,
- * f16(f32(y) + that)), with the reference's f16 block accumulation. */
+ * f16(f32(y) + that)). Arithmetic (environment BP_MATVEC_ARITH at
+ * bp_model_create): "f16" = the reference's f16 block sums, bit for bit;
+ * "mfma" = exact integer sums of x rounded to 15 bits of each block's max |x|,
+ * f32 scaling; default "auto" = f16 below 32768 rows, mfma from there on. */
 bp_status bp_dispatch_matvec_q1_0(bp_model* model, const void* weights, void* act, uint32_t k,
                                   uint32_t n, uint32_t w_d, uint32_t w_qs, uint32_t in_off,
                                   uint32_t out_off, uint32_t accumulate);
@@ -162,7 +165,7 @@ typedef struct {
 } bp_matvec_range;
 /* rms_norm(x) * w_norm followed by 2 or 3 Q1_0 matvecs sharing x
  * (src/shaders/matvec_q1_0_fused_normed.wgsl, src/forward.rs:284-334); every
- * range's n is a multiple of 32 (the reference asks for 16). */
+ * range's n is a multiple of 16, 1 to 3 ranges. */
 bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* model, const void* weights, void* act,
                                                const void* w_norms, uint32_t k, uint32_t in_off,
                                                uint32_t w_norm_off, uint32_t n_ranges,

@@ -319,6 +319,7 @@ def test_matvec_silu(cuda, monkeypatch, arith, n, k, acc):
     [(Q_DIM, 0), (KV_DIM, 1), (KV_DIM, 2)],          # q / k / v from attn_norm(x)
     [(FFN, 0), (FFN, 1)],                            # gate / up from ffn_norm(x)
     [(96, 0)],
+    [(48, 0), (16, 1), (80, 2)],                     # multiples of 16 only
 ])
 def test_matvec_fused_normed(cuda, monkeypatch, arith, ranges):
     k = HIDDEN
@@ -405,4 +406,4 @@ def test_matvec_rejects_bad_shapes(cuda, monkeypatch):
         m.dispatch_matvec_q1_0(w.data_ptr(), a.data_ptr(), 256, 32, 1, 0, 0, 0, False)
     with pytest.raises(PotError):
         m.dispatch_matvec_q1_0_fused_normed(w.data_ptr(), a.data_ptr(), a.data_ptr(), 256, 0, 0,
-                                            [(0, 0, 33, 0)])
+                                            [(0, 0, 24, 0)])

@@ -76,6 +76,8 @@ _SIGS = {
     "bp_dispatch_matvec_q1_0_silu": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_matvec_q1_0_fused_normed": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                                      ctypes.POINTER(MatvecRange)]),
+    "bp_dispatch_quantize_act": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_matmul_q1_0": (_i32, [_vp, _vp, _vp, _vp] + [_u32] * 9),
     "bp_kv_snapshot_payload_bytes": (_u64, [_u32, _u32, _u32]),
     "bp_kv_snapshot_capture": (_i32, [_vp, _u32, _vp, _u64]),
     "bp_kv_snapshot_apply": (_i32, [_vp, _u32, _vp, _u64]),
@@ -200,6 +202,16 @@ class Model:
         arr = (MatvecRange * max(1, len(ranges)))(*[MatvecRange(*r) for r in ranges])
         _check(lib.bp_dispatch_matvec_q1_0_fused_normed(self._h, weights, act, w_norms, k, input_offset,
                                                         w_norm_off, len(ranges), arr))
+
+    # -- prefill projections (src/forward.rs:415-472) -----------------------------
+    def dispatch_quantize_act(self, act: int, acts_q8: int, k: int, m_tokens: int, in_off: int, d_off: int,
+                              qs_off: int) -> None:
+        _check(lib.bp_dispatch_quantize_act(self._h, act, acts_q8, k, m_tokens, in_off, d_off, qs_off))
+
+    def dispatch_matmul_q1_0(self, weights: int, acts_q8: int, act: int, k: int, n: int, m_tokens: int,
+                             w_d: int, w_qs: int, a_d: int, a_qs: int, out_off: int, accumulate: bool) -> None:
+        _check(lib.bp_dispatch_matmul_q1_0(self._h, weights, acts_q8, act, k, n, m_tokens, w_d, w_qs, a_d, a_qs,
+                                           out_off, 1 if accumulate else 0))
 
     # -- snapshot payload (src/kv_snapshot.rs:203-372) ----------------------------
     def snapshot_payload(self, pos: int) -> bytes:

@@ -576,6 +576,56 @@ bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* m, const void* weights,
     return hip_check(m, launch_matvec(m, a, 2), "matvec_q1_0_fused_normed launch");
 }
 
+bp_status bp_dispatch_quantize_act(bp_model* m, const void* act, void* acts_q8, uint32_t k, uint32_t n_tokens,
+                                   uint32_t in_off, uint32_t d_off, uint32_t qs_off) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act || !acts_q8) return fail(BP_ERR_INVALID_ARG, "act/acts_q8 is NULL");
+    if (k == 0 || k % 32 != 0) return fail(BP_ERR_INVALID_ARG, "quantize k = %u must be a positive multiple of 32", k);
+    if ((d_off | qs_off) & 3u)
+        return fail(BP_ERR_INVALID_ARG, "quantize d/qs offsets (%u, %u) must be multiples of 4", d_off, qs_off);
+    if (n_tokens == 0) return BP_OK;
+    if (static_cast<uint64_t>(n_tokens) * (k / 32) > 0xFFFFFFFFull / 8)
+        return fail(BP_ERR_INVALID_ARG, "quantize: %u x %u too large", n_tokens, k);
+    bp::QuantArgs a{};
+    a.act = static_cast<const uint16_t*>(act);
+    a.out = static_cast<uint8_t*>(acts_q8);
+    a.k = k;
+    a.m = n_tokens;
+    a.input_offset = in_off;
+    a.d_offset = d_off;
+    a.qs_offset = qs_off;
+    return hip_check(m, bp::launch_quantize_act_q8_0(a, m->stream), "quantize_act_q8_0 launch");
+}
+
+bp_status bp_dispatch_matmul_q1_0(bp_model* m, const void* weights, const void* acts_q8, void* act, uint32_t k,
+                                  uint32_t n, uint32_t n_tokens, uint32_t w_d, uint32_t w_qs, uint32_t a_d,
+                                  uint32_t a_qs, uint32_t out_off, uint32_t accumulate) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!weights || !acts_q8 || !act) return fail(BP_ERR_INVALID_ARG, "weights/acts_q8/act is NULL");
+    if (k == 0 || k % 128 != 0) return fail(BP_ERR_INVALID_ARG, "matmul k = %u must be a positive multiple of 128", k);
+    if ((w_d & 1u) || (w_qs & 3u) || (a_d & 3u) || (a_qs & 3u))
+        return fail(BP_ERR_INVALID_ARG, "matmul offsets: w_d 2-byte, w_qs / a_d / a_qs 4-byte aligned (%u, %u, %u, %u)",
+                    w_d, w_qs, a_d, a_qs);
+    if (n == 0 || n_tokens == 0) return BP_OK;
+    if ((n_tokens + 63) / 64 > 65535) return fail(BP_ERR_INVALID_ARG, "matmul: %u tokens too many", n_tokens);
+    bp::MatmulArgs a{};
+    a.weights = static_cast<const uint8_t*>(weights);
+    a.acts = static_cast<const uint8_t*>(acts_q8);
+    a.y = static_cast<uint16_t*>(act);
+    a.k = k;
+    a.n = n;
+    a.m = n_tokens;
+    a.w_d_offset = w_d;
+    a.w_qs_offset = w_qs;
+    a.a_d_offset = a_d;
+    a.a_qs_offset = a_qs;
+    a.out_offset = out_off;
+    a.accumulate = accumulate ? 1u : 0u;
+    return hip_check(m, bp::launch_matmul_q1_0_q8_0(a, m->stream), "matmul_q1_0_q8_0 launch");
+}
+
 static bp_status snapshot_copy(bp_model* m, uint32_t pos, uint8_t* payload, uint64_t payload_bytes,
                                bool to_host) {
     bp_status st = enter(m);

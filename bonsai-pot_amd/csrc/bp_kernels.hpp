@@ -122,6 +122,26 @@ hipError_t launch_matvec_q1_0(const MatvecArgs& a, int mode, hipStream_t s);
 hipError_t launch_matvec_q1_0_mfma(const MatvecArgs& a, int mode, hipStream_t s);
 uint32_t matvec_max_k();
 
+// Prefill projections (quantize_q8_0 / matmul_q1_0_q8_0).
+struct QuantArgs {
+    const uint16_t* act;      // f16 activations
+    uint8_t* out;             // Q8_0 buffer (bytes)
+    uint32_t k, m;            // k multiple of 32
+    uint32_t input_offset;    // f16 elements
+    uint32_t d_offset, qs_offset;   // bytes, multiples of 4
+};
+struct MatmulArgs {
+    const uint8_t* weights;   // Q1_0 weight buffer (bytes)
+    const uint8_t* acts;      // Q8_0 activation buffer (bytes)
+    uint16_t* y;              // f16 output buffer
+    uint32_t k, n, m;         // k multiple of 128
+    uint32_t w_d_offset, w_qs_offset, a_d_offset, a_qs_offset;   // bytes
+    uint32_t out_offset;      // f16 elements
+    uint32_t accumulate;
+};
+hipError_t launch_quantize_act_q8_0(const QuantArgs& a, hipStream_t s);
+hipError_t launch_matmul_q1_0_q8_0(const MatmulArgs& a, hipStream_t s);
+
 hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t m_tokens,
                               hipStream_t s);
 hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uint32_t m_tokens,

@@ -16,6 +16,8 @@
  *   bp_dispatch_matvec_q1_0_silu     <- dispatch_matvec_q1_0_silu    src/forward.rs:243-282
  *   bp_dispatch_matvec_q1_0_fused_normed <- dispatch_matvec_q1_0_fused_normed
  *                                       src/forward.rs:284-334
+ *   bp_dispatch_quantize_act         <- dispatch_quantize_act        src/forward.rs:415-441
+ *   bp_dispatch_matmul_q1_0          <- dispatch_matmul_q1_0         src/forward.rs:443-472
  *   bp_model_create / _destroy       <- KV / RoPE / partials part of Model::load_with_options
  *                                       src/model.rs:1148-1248
  *   bp_kv_snapshot_capture / _apply  <- kv_snapshot::capture / apply src/kv_snapshot.rs:203-372
@@ -170,6 +172,23 @@ bp_status bp_dispatch_matvec_q1_0_fused_normed(bp_model* model, const void* weig
                                                const void* w_norms, uint32_t k, uint32_t in_off,
                                                uint32_t w_norm_off, uint32_t n_ranges,
                                                const bp_matvec_range* ranges);
+
+/* Prefill projections (src/shaders/quantize_q8_0.wgsl, matmul_q1_0_q8_0.wgsl).
+ * quantize: act[in_off + t*k ..] (f16, t < n_tokens) to Q8_0 in the byte
+ * buffer acts_q8: f32 d of block (t, b) at d_off + 4*(t*k/32 + b), qs at
+ * qs_off + t*k + 32*b; k a multiple of 32, offsets multiples of 4
+ * (src/forward.rs:415-441 uses d_off = 0, qs_off = n_tokens*k/32*4). */
+bp_status bp_dispatch_quantize_act(bp_model* model, const void* act, void* acts_q8, uint32_t k,
+                                   uint32_t n_tokens, uint32_t in_off, uint32_t d_off, uint32_t qs_off);
+/* y[out_off + t*n + r] = f16(sum over 128-blocks b, then 32-blocks s, of
+ * (a_d * w_d) * f32(sumi)) in f32, bit for bit the reference's arithmetic
+ * (sumi: exact sum of +-q); with accumulate f16(f32(y) + that). Weights as in
+ * the matvecs (byte offsets w_d / w_qs), activations as written by
+ * bp_dispatch_quantize_act (byte offsets a_d / a_qs); k a multiple of 128
+ * (src/forward.rs:443-472). */
+bp_status bp_dispatch_matmul_q1_0(bp_model* model, const void* weights, const void* acts_q8, void* act,
+                                  uint32_t k, uint32_t n, uint32_t n_tokens, uint32_t w_d, uint32_t w_qs,
+                                  uint32_t a_d, uint32_t a_qs, uint32_t out_off, uint32_t accumulate);
 
 /* BONSAIKV v1 payload (src/kv_snapshot.rs:8-20): for kind in {K, V}, for each
  * layer: pos*(kv_dim/32)*4 bytes of d, then pos*kv_dim bytes of qs.

@@ -544,6 +544,56 @@ void bpo_matvec_q1_0_fused_normed(const bpo_matvec_fused_normed_params* p, const
     free(x);
 }
 
+/* quantize_q8_0.wgsl:49-86: one workgroup per (row, 32-block); the quantizer
+ * is the one of kv_writeback (amax / 127, RNE, clamp +-127). */
+void bpo_quantize_act_q8_0(const bpo_quant_params* p, const uint16_t* act, uint8_t* outbuf) {
+    const uint32_t nb = p->k / 32;
+    for (uint32_t row = 0; row < p->m; row++)
+        for (uint32_t b = 0; b < nb; b++) {
+            float x[32], d;
+            int8_t q[32];
+            for (int i = 0; i < 32; i++)
+                x[i] = bpo_f16_to_f32(act[p->input_offset + (uint64_t)row * p->k + 32u * b + (uint32_t)i]);
+            bpo_quantize_q8_0_block(x, &d, q);
+            memcpy(outbuf + p->d_offset + 4 * ((uint64_t)row * nb + b), &d, 4);
+            memcpy(outbuf + p->qs_offset + (uint64_t)row * p->k + 32u * b, q, 32);
+        }
+}
+
+/* matmul_q1_0_q8_0.wgsl:78-262: for each (row, col): acc over 128-blocks b
+ * (outer) and their four 32-blocks s (inner) of (a_d * w_d) * f32(sumi), where
+ * sumi = sum of (bit ? +q : -q) over the 32 elements (exact); then the f16
+ * store, or f16(f32(y) + acc) with accumulate. */
+void bpo_matmul_q1_0_q8_0(const bpo_matmul_params* p, const uint8_t* weights, const uint8_t* acts,
+                          uint16_t* y) {
+    const uint32_t nb1 = p->k / 128, nb8 = p->k / 32;
+    for (uint32_t row = 0; row < p->m; row++)
+        for (uint32_t col = 0; col < p->n; col++) {
+            float acc = 0.0f;
+            for (uint32_t b = 0; b < nb1; b++) {
+                uint16_t wdh;
+                memcpy(&wdh, weights + p->w_d_offset + 2 * ((uint64_t)col * nb1 + b), 2);
+                const float wd = bpo_f16_to_f32(wdh);
+                const uint8_t* bits = weights + p->w_qs_offset + ((uint64_t)col * nb1 + b) * 16;
+                for (uint32_t s = 0; s < 4; s++) {
+                    float ad;
+                    memcpy(&ad, acts + p->a_d_offset + 4 * ((uint64_t)row * nb8 + 4 * b + s), 4);
+                    const int8_t* q = (const int8_t*)(acts + p->a_qs_offset + (uint64_t)row * p->k + 128u * b + 32u * s);
+                    int32_t sumi = 0;
+                    for (uint32_t e = 0; e < 32; e++) {
+                        const uint32_t bit = (bits[(32 * s + e) / 8] >> ((32 * s + e) % 8)) & 1u;
+                        sumi += bit ? q[e] : -q[e];
+                    }
+                    const float scale = ad * wd;
+                    const float v = scale * (float)sumi;
+                    acc = acc + v;
+                }
+            }
+            const uint64_t yi = p->out_offset + (uint64_t)row * p->n + col;
+            y[yi] = p->accumulate ? bpo_f32_to_f16(bpo_f16_to_f32(y[yi]) + acc) : bpo_f32_to_f16(acc);
+        }
+}
+
 static uint64_t splitmix64(uint64_t* s) {
     uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;

@@ -134,6 +134,24 @@ void bpo_matvec_q1_0_silu(const bpo_matvec_silu_params* p, const uint8_t* weight
 void bpo_matvec_q1_0_fused_normed(const bpo_matvec_fused_normed_params* p, const uint8_t* weights,
                                   uint16_t* act, const uint16_t* w_norms);
 
+/* ---- prefill projections: Q8_0 activations x Q1_0 weights ----------------- */
+typedef struct {            /* QuantParams, src/model.rs:172-179 (no dispatch_x_dim) */
+    uint32_t k, m, input_offset, d_offset, qs_offset;
+} bpo_quant_params;
+/* src/shaders/quantize_q8_0.wgsl: act[input_offset + m*k ..] (f16 elements) to
+ * Q8_0 in `outbuf` (bytes): f32 d of block (row, b) at d_offset + 4*(row*k/32 + b),
+ * qs at qs_offset + row*k + 32*b. */
+void bpo_quantize_act_q8_0(const bpo_quant_params* p, const uint16_t* act, uint8_t* outbuf);
+
+typedef struct {            /* MatmulParams, src/model.rs:182-192 */
+    uint32_t k, n, m, w_d_offset, w_qs_offset, a_d_offset, a_qs_offset, out_offset, accumulate;
+} bpo_matmul_params;
+/* src/shaders/matmul_q1_0_q8_0.wgsl: y[out_offset + row*n + col] (f16) =
+ * sum over 128-blocks b, then 32-blocks s of (a_d * w_d) * f32(sumi), in f32,
+ * sumi the exact integer sum of +-q over the 32 elements. */
+void bpo_matmul_q1_0_q8_0(const bpo_matmul_params* p, const uint8_t* weights, const uint8_t* acts,
+                          uint16_t* y);
+
 /* ---- seeded synthetic inputs (splitmix64 + Box-Muller) -------------------- */
 void bpo_fill_normal_f16(uint64_t seed, float mean, float stddev, uint16_t* out, size_t n);
 

@@ -76,6 +76,17 @@ class MatvecFusedNormedParams(ctypes.Structure):
                 ("output_offset", _u32 * 3)]
 
 
+class QuantParams(ctypes.Structure):
+    """QuantParams, src/model.rs:172-179 (without dispatch_x_dim)."""
+    _fields_ = [(n, _u32) for n in ("k", "m", "input_offset", "d_offset", "qs_offset")]
+
+
+class MatmulParams(ctypes.Structure):
+    """MatmulParams, src/model.rs:182-192."""
+    _fields_ = [(n, _u32) for n in ("k", "n", "m", "w_d_offset", "w_qs_offset", "a_d_offset", "a_qs_offset",
+                                     "out_offset", "accumulate")]
+
+
 def _sig(name, res, args):
     f = getattr(_lib, name)
     f.restype, f.argtypes = res, args
@@ -104,6 +115,8 @@ _split = _sig("bpo_attention_split_merge", None, [ctypes.POINTER(AttnSplitParams
 _attn = _sig("bpo_attention", None, [ctypes.POINTER(AttnParams), _vp, _vp, _vp, _vp, _u32, _vp,
                                     _vp])
 _fill = _sig("bpo_fill_normal_f16", None, [_u64, _f32, _f32, _vp, ctypes.c_size_t])
+_quant_act = _sig("bpo_quantize_act_q8_0", None, [ctypes.POINTER(QuantParams), _vp, _vp])
+_matmul = _sig("bpo_matmul_q1_0_q8_0", None, [ctypes.POINTER(MatmulParams), _vp, _vp, _vp])
 _f16_add = _sig("bpo_f16_add", ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16])
 _f16_mul = _sig("bpo_f16_mul", ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16])
 _mv = _sig("bpo_matvec_q1_0", None, [ctypes.POINTER(MatvecParams), _vp, _vp])
@@ -272,3 +285,19 @@ def q1_0_tensor(rng: np.random.Generator, n: int, k: int, d_scale=0.02):
     buf[:d_bytes.size] = d_bytes
     buf[qs_off:] = qs
     return buf, 0, qs_off
+
+
+# ---- prefill projections (quantize_q8_0.wgsl, matmul_q1_0_q8_0.wgsl) ---------
+def quantize_act_q8_0(p: QuantParams, act, outbuf: np.ndarray) -> np.ndarray:
+    """Returns a copy of outbuf (uint8) with the Q8_0 d / qs regions written."""
+    out = np.ascontiguousarray(outbuf, np.uint8).copy()
+    _quant_act(ctypes.byref(p), _ptr(_u16(act)), _ptr(out))
+    return out
+
+
+def matmul_q1_0_q8_0(p: MatmulParams, weights: np.ndarray, acts: np.ndarray, y) -> np.ndarray:
+    """Returns a copy of y (uint16, the f16 activation buffer) with the output written."""
+    out = _u16(y).copy()
+    _matmul(ctypes.byref(p), _ptr(np.ascontiguousarray(weights, np.uint8)),
+            _ptr(np.ascontiguousarray(acts, np.uint8)), _ptr(out))
+    return out

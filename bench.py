@@ -14,7 +14,9 @@ Also reported: decode at ctx 32768 (config 5, rotating over 8 layers),
 prefill pp2048 (metric) and the 2048-on-2048 chunked prefill (config 4) in
 TFLOP/s of unmasked QK^T + PV work, the Bonsai-4B per-layer Q1_0 decode
 matvecs (fused normed q/k/v, o, fused normed gate/up, silu down) over 36
-layers of distinct weights in GB/s, and the CPU oracle on a bounded sample.
+layers of distinct weights in GB/s, the prefill projections (Q8_0
+quantize + Q1_0 x Q8_0 matmul) of a Bonsai-4B layer at 512 tokens in TOPS,
+and the CPU oracle on a bounded sample.
 """
 import argparse
 import json
@@ -28,6 +30,7 @@ sys.path.insert(0, os.path.join(ROOT, "bonsai-pot_amd"))
 METRIC = "decode-attn HBM GB/s (%peak) ctx4K/32K; prefill-attn TFLOP/s (%MFMA) pp2048"
 HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2500.0
+I8_MFMA_PEAK_TOPS = 5000.0
 KV_ROW_BYTES = 2 * 8 * (128 + 16)   # 2304 B per cache row: K + V, 8 KV heads, 128 qs + 4 f32 d
 QO_BYTES = 2 * 32 * 128 * 2         # q in + out, f16
 
@@ -48,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode4k", "decode32k", "prefill", "chunked", "matvec", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode4k", "decode32k", "prefill", "chunked", "matvec", "matmul", "copy"], default=None,
                     help="run only one workload (for profiling)")
     return ap.parse_args()
 
@@ -357,9 +360,62 @@ def bench_lm_head(torch, args, vocab=151936, n_copies=8):
     torch.cuda.synchronize()
     us = per_launch_us(torch, _B, launch, 2 * n_copies)
     byt = int(vocab * H * Q1_BYTES_PER_WEIGHT) + 2 * (H + vocab)
+    # top-k (k = 32) of the head's logits, as the step's last dispatch
+    res = torch.zeros(64, dtype=torch.int32, device="cuda")
+    topk = lambda i: m.dispatch_topk_reduce(act.data_ptr(), res.data_ptr(), vocab, 32, H, 0)
+    topk(0)
+    torch.cuda.synchronize()
+    tk_us = per_launch_us(torch, _B, topk, 8)
     m.close()
     return {"n_k": [vocab, H], "kernel_us_avg": us, "bytes": byt, "GBps": byt / (us * 1e-6) / 1e9,
-            "frac_hbm": byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+            "frac_hbm": byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "topk_reduce_k32": {"n": vocab, "us_avg": tk_us, "bytes": 2 * vocab,
+                                "note": "2 launches (per-lane heaps, merge tree); latency-bound"}}
+
+
+def bench_matmul(torch, args, m_tokens=512, n_layer=8):
+    """The Bonsai-4B prefill projections of one layer at m_tokens tokens:
+    quantize_act (Q8_0) of each input, then the Q1_0 x Q8_0 matmul (q/k/v
+    6144x2560, o 2560x4096, gate/up 19456x2560, down 2560x9728), over n_layer
+    layers of distinct weights. Work = 2 m n k integer ops per matmul
+    (i8 MFMA peak 5.0 POP/s)."""
+    b = MatvecLayers(torch, n_layer, seed=3)
+    m = b.model
+    g = torch.Generator(device="cuda").manual_seed(11)
+    kmax = max(k for _, k in b.tensors.values())
+    nmax = max(n for n, _ in b.tensors.values())
+    x = torch.randn(m_tokens * kmax, generator=g, device="cuda").to(torch.float16)
+    y = torch.zeros(m_tokens * nmax, device="cuda", dtype=torch.float16)
+    q8 = torch.empty(m_tokens * kmax + m_tokens * kmax // 8, device="cuda", dtype=torch.int8)
+    qs_off = m_tokens * kmax // 8
+
+    def quant(name):
+        _, k = b.tensors[name]
+        m.dispatch_quantize_act(x.data_ptr(), q8.data_ptr(), k, m_tokens, 0, 0, qs_off)
+
+    def mm(name, il):
+        n, k = b.tensors[name]
+        d_off, w_qs = b.offs[name]
+        m.dispatch_matmul_q1_0(b.bufs[il].data_ptr(), q8.data_ptr(), y.data_ptr(), k, n, m_tokens,
+                               d_off, w_qs, 0, qs_off, 0, name in ("o", "down"))
+
+    res = {"m_tokens": m_tokens, "layers": n_layer}
+    total_us, total_ops = 0.0, 0
+    for nm, (n, k) in b.tensors.items():
+        quant(nm)
+        mm(nm, 0)
+        torch.cuda.synchronize()
+        us = per_launch_us(torch, b, lambda i, nm=nm: mm(nm, i % n_layer), n_layer)
+        q_us = per_launch_us(torch, b, lambda i, nm=nm: quant(nm), 4)
+        ops = 2 * m_tokens * n * k
+        total_us += us + q_us
+        total_ops += ops
+        res[nm] = {"n_k": [n, k], "matmul_us_avg": us, "quantize_us_avg": q_us, "ops": ops,
+                   "TOPS": ops / (us * 1e-6) / 1e12, "frac_i8_mfma": ops / (us * 1e-6) / 1e12 / I8_MFMA_PEAK_TOPS}
+    res["layer_us"] = total_us
+    res["layer_TOPS"] = total_ops / (total_us * 1e-6) / 1e12
+    m.close()
+    return res
 
 
 def measured_traffic(workload, kernel):
@@ -450,6 +506,8 @@ def main():
         extras["chunked_prefill_2048_on_2048"] = bench_prefill(torch, args, 2048, 2048)
     if args.only in (None, "matvec"):
         extras["matvec_q1_0_4b_layer"] = bench_matvec(torch, args)
+    if args.only in (None, "matmul"):
+        extras["matmul_q1_0_q8_0_4b_layer_pp512"] = bench_matmul(torch, args)
     if args.only == "copy":
         extras["copy_1GiB"] = bench_copy(torch, args)
     if args.only is not None:

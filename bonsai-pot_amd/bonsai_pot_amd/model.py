@@ -78,6 +78,8 @@ _SIGS = {
                                                      ctypes.POINTER(MatvecRange)]),
     "bp_dispatch_quantize_act": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_matmul_q1_0": (_i32, [_vp, _vp, _vp, _vp] + [_u32] * 9),
+    "bp_dispatch_topk_reduce": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "bp_topk_readback": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "bp_kv_snapshot_payload_bytes": (_u64, [_u32, _u32, _u32]),
     "bp_kv_snapshot_capture": (_i32, [_vp, _u32, _vp, _u64]),
     "bp_kv_snapshot_apply": (_i32, [_vp, _u32, _vp, _u64]),
@@ -212,6 +214,19 @@ class Model:
                              w_d: int, w_qs: int, a_d: int, a_qs: int, out_off: int, accumulate: bool) -> None:
         _check(lib.bp_dispatch_matmul_q1_0(self._h, weights, acts_q8, act, k, n, m_tokens, w_d, w_qs, a_d, a_qs,
                                            out_off, 1 if accumulate else 0))
+
+    # -- top-k (src/forward.rs:336-354, :542-568) ---------------------------------
+    def dispatch_topk_reduce(self, act: int, result: int, n: int, k: int, in_off: int, out_off: int) -> None:
+        _check(lib.bp_dispatch_topk_reduce(self._h, act, result, n, k, in_off, out_off))
+
+    def wait_topk_readback(self, result: int, out_off: int, k: int):
+        """(values f32[k], indices u32[k]) after the stream drains, as wait_topk_readback."""
+        import numpy as np
+        vals = np.zeros(k, np.float32)
+        idx = np.zeros(k, np.uint32)
+        _check(lib.bp_topk_readback(self._h, result, out_off, k, vals.ctypes.data_as(_vp),
+                                    idx.ctypes.data_as(_vp)))
+        return vals, idx
 
     # -- snapshot payload (src/kv_snapshot.rs:203-372) ----------------------------
     def snapshot_payload(self, pos: int) -> bytes:

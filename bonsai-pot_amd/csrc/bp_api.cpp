@@ -40,6 +40,7 @@ struct bp_model {
     uint64_t partials_floats;
     uint16_t* kv16;       // prefill: f16 image of one layer's K and V (prefill_image_bytes)
     uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
+    void* topk_lists;     // top-k scratch: 256 sorted lists of 32 {value, index}
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
     int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 f16 sums in the reference's order, 2 i8 MFMA
@@ -273,7 +274,8 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
         hipMalloc(&m->rope_cs, rope_elems * 2) != hipSuccess ||
         hipMalloc(&m->partials, m->partials_floats * 4) != hipSuccess ||
         hipMalloc(&m->q_norm, static_cast<size_t>(cfg->n_head) * cfg->head_dim * 2) != hipSuccess ||
-        hipMalloc(&m->kv16, bp::prefill_image_bytes(cfg->n_kv_head, max_seq)) != hipSuccess) {
+        hipMalloc(&m->kv16, bp::prefill_image_bytes(cfg->n_kv_head, max_seq)) != hipSuccess ||
+        hipMalloc(&m->topk_lists, bp::topk_scratch_bytes()) != hipSuccess) {
         (void)hipGetLastError();
         return bail(fail(BP_ERR_OUT_OF_MEMORY, "hipMalloc failed for KV cache of %llu bytes x2",
                          static_cast<unsigned long long>(m->kv_bytes)));
@@ -299,6 +301,7 @@ void bp_model_destroy(bp_model* m) {
         if (m->partials) (void)hipFree(m->partials);
         if (m->kv16) (void)hipFree(m->kv16);
         if (m->q_norm) (void)hipFree(m->q_norm);
+        if (m->topk_lists) (void)hipFree(m->topk_lists);
     }
     (void)hipGetLastError();
     delete m;
@@ -624,6 +627,39 @@ bp_status bp_dispatch_matmul_q1_0(bp_model* m, const void* weights, const void* 
     a.out_offset = out_off;
     a.accumulate = accumulate ? 1u : 0u;
     return hip_check(m, bp::launch_matmul_q1_0_q8_0(a, m->stream), "matmul_q1_0_q8_0 launch");
+}
+
+bp_status bp_dispatch_topk_reduce(bp_model* m, const void* act, void* result, uint32_t n, uint32_t k,
+                                  uint32_t in_off, uint32_t out_off) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act || !result) return fail(BP_ERR_INVALID_ARG, "act/result is NULL");
+    if (in_off & 1u) return fail(BP_ERR_INVALID_ARG, "topk in_offset %u must be even (f16 pairs)", in_off);
+    if (static_cast<uint64_t>(n) + in_off > 0xFFFFFFFFull)
+        return fail(BP_ERR_INVALID_ARG, "topk: n %u + in_offset %u overflows u32", n, in_off);
+    bp::TopKArgs a{};
+    a.logits = static_cast<const uint16_t*>(act);
+    a.result = static_cast<uint32_t*>(result);
+    a.lists = static_cast<uint2*>(m->topk_lists);
+    a.n = n;
+    a.in_offset = in_off;
+    a.out_offset = out_off;
+    a.k = k;
+    return hip_check(m, bp::launch_topk_reduce(a, m->stream), "topk_reduce launch");
+}
+
+bp_status bp_topk_readback(bp_model* m, const void* result, uint32_t out_off, uint32_t k, float* values,
+                           uint32_t* indices) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!result || (k && (!values || !indices))) return fail(BP_ERR_INVALID_ARG, "result/values/indices is NULL");
+    if (k > 32) return fail(BP_ERR_INVALID_ARG, "topk readback k = %u exceeds 32", k);
+    if ((st = hip_check(m, hipStreamSynchronize(m->stream), "topk readback sync")) != BP_OK) return st;
+    if (k == 0) return BP_OK;
+    const uint32_t* src = static_cast<const uint32_t*>(result) + out_off;
+    if ((st = hip_check(m, hipMemcpy(values, src, 4ull * k, hipMemcpyDeviceToHost), "topk readback values")) != BP_OK)
+        return st;
+    return hip_check(m, hipMemcpy(indices, src + k, 4ull * k, hipMemcpyDeviceToHost), "topk readback indices");
 }
 
 static bp_status snapshot_copy(bp_model* m, uint32_t pos, uint8_t* payload, uint64_t payload_bytes,

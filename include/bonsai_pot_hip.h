@@ -18,6 +18,8 @@
  *                                       src/forward.rs:284-334
  *   bp_dispatch_quantize_act         <- dispatch_quantize_act        src/forward.rs:415-441
  *   bp_dispatch_matmul_q1_0          <- dispatch_matmul_q1_0         src/forward.rs:443-472
+ *   bp_dispatch_topk_reduce          <- dispatch_topk_reduce         src/forward.rs:336-354
+ *   bp_topk_readback                 <- wait_topk_readback           src/forward.rs:542-568
  *   bp_model_create / _destroy       <- KV / RoPE / partials part of Model::load_with_options
  *                                       src/model.rs:1148-1248
  *   bp_kv_snapshot_capture / _apply  <- kv_snapshot::capture / apply src/kv_snapshot.rs:203-372
@@ -189,6 +191,21 @@ bp_status bp_dispatch_quantize_act(bp_model* model, const void* act, void* acts_
 bp_status bp_dispatch_matmul_q1_0(bp_model* model, const void* weights, const void* acts_q8, void* act,
                                   uint32_t k, uint32_t n, uint32_t n_tokens, uint32_t w_d, uint32_t w_qs,
                                   uint32_t a_d, uint32_t a_qs, uint32_t out_off, uint32_t accumulate);
+
+/* Top-k of n f16 logits at act[in_off ..] (in_off even), same values and
+ * indices as src/shaders/topk_reduce.wgsl, ties included (the reference's
+ * per-thread heaps and bitonic merge tree are kept step for step):
+ * result[out_off + i] = f32 bits of the i-th largest value (descending),
+ * result[out_off + kk + i] = its index, kk = min(k, 32); if fewer than kk
+ * logits exceed -1e30 the rest are -1e30 / index 0. `result` is a u32 device
+ * buffer. Replaces dispatch_topk_reduce (src/forward.rs:336-354). */
+bp_status bp_dispatch_topk_reduce(bp_model* model, const void* act, void* result, uint32_t n, uint32_t k,
+                                  uint32_t in_off, uint32_t out_off);
+/* Waits for the model's stream, then copies the k values (f32) and k indices
+ * written by bp_dispatch_topk_reduce (with the same k <= 32) to host memory.
+ * Replaces wait_topk_readback (src/forward.rs:542-568). */
+bp_status bp_topk_readback(bp_model* model, const void* result, uint32_t out_off, uint32_t k, float* values,
+                           uint32_t* indices);
 
 /* BONSAIKV v1 payload (src/kv_snapshot.rs:8-20): for kind in {K, V}, for each
  * layer: pos*(kv_dim/32)*4 bytes of d, then pos*kv_dim bytes of qs.

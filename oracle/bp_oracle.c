@@ -611,3 +611,82 @@ void bpo_fill_normal_f16(uint64_t seed, float mean, float stddev, uint16_t* out,
         if (i + 1 < n) out[i + 1] = bpo_f32_to_f16((float)(mean + stddev * r * sin(two_pi * u2)));
     }
 }
+
+/* ---- src/shaders/topk_reduce.wgsl ----------------------------------------- */
+#define TOPK_LANES 256u   /* WG, topk_reduce.wgsl:34 */
+#define TOPK_KMAX 32u     /* K_MAX, topk_reduce.wgsl:35 */
+
+/* Min-heap sift-down over heap[0 .. len) (topk_reduce.wgsl:42-55, :103-113):
+ * the left child wins ties, a strictly smaller child is swapped up. */
+static void topk_sift(float* v, uint32_t* ix, uint32_t len) {
+    uint32_t i = 0;
+    for (;;) {
+        const uint32_t l = 2 * i + 1, r = l + 1;
+        uint32_t m = i;
+        if (l < len && v[l] < v[m]) m = l;
+        if (r < len && v[r] < v[m]) m = r;
+        if (m == i) return;
+        const float tv = v[i]; v[i] = v[m]; v[m] = tv;
+        const uint32_t ti = ix[i]; ix[i] = ix[m]; ix[m] = ti;
+        i = m;
+    }
+}
+
+void bpo_topk_reduce(const bpo_topk_params* p, const uint16_t* act, uint32_t* result) {
+    float* v = malloc(sizeof(float) * TOPK_LANES * TOPK_KMAX);
+    uint32_t* ix = malloc(sizeof(uint32_t) * TOPK_LANES * TOPK_KMAX);
+    if (!v || !ix) abort();
+    const uint32_t n_words = (p->n + 1) / 2;
+    const uint16_t* x = act + (p->in_offset & ~1u);
+    /* phase 1 (:65-96) and 2a (:98-115): independent per lane */
+    for (uint32_t t = 0; t < TOPK_LANES; t++) {
+        float* hv = v + t * TOPK_KMAX;
+        uint32_t* hi = ix + t * TOPK_KMAX;
+        for (uint32_t i = 0; i < TOPK_KMAX; i++) { hv[i] = -1e30f; hi[i] = 0; }
+        for (uint32_t w = t; w < n_words; w += TOPK_LANES) {
+            for (uint32_t h = 0; h < 2; h++) {
+                const uint32_t e = 2 * w + h;
+                if (h == 1 && e >= p->n) break;
+                const float val = bpo_f16_to_f32(x[e]);
+                if (val > hv[0]) { hv[0] = val; hi[0] = e; topk_sift(hv, hi, TOPK_KMAX); }
+            }
+        }
+        for (uint32_t last = TOPK_KMAX - 1; last > 0; last--) {
+            const float tv = hv[0]; hv[0] = hv[last]; hv[last] = tv;
+            const uint32_t ti = hi[0]; hi[0] = hi[last]; hi[last] = ti;
+            topk_sift(hv, hi, last);
+        }
+    }
+    /* phase 2b (:117-184): list p absorbs list p + s, s = 128, 64, .., 1 */
+    for (uint32_t s = TOPK_LANES / 2; s > 0; s /= 2) {
+        for (uint32_t pr = 0; pr < s; pr++) {
+            float* av = v + pr * TOPK_KMAX;
+            uint32_t* ai = ix + pr * TOPK_KMAX;
+            const float* bv = v + (pr + s) * TOPK_KMAX;
+            const uint32_t* bi = ix + (pr + s) * TOPK_KMAX;
+            for (uint32_t i = 0; i < TOPK_KMAX; i++) {   /* stage 0: a[i] vs b[31-i] */
+                const uint32_t j = TOPK_KMAX - 1 - i;
+                if (bv[j] > av[i]) { av[i] = bv[j]; ai[i] = bi[j]; }
+            }
+            for (uint32_t stride = TOPK_KMAX / 2; stride > 0; stride /= 2) {
+                for (uint32_t lo = 0; lo < TOPK_KMAX; lo++) {
+                    if (lo & stride) continue;
+                    const uint32_t hi = lo | stride;
+                    if (av[hi] > av[lo]) {
+                        const float tv = av[lo]; av[lo] = av[hi]; av[hi] = tv;
+                        const uint32_t ti = ai[lo]; ai[lo] = ai[hi]; ai[hi] = ti;
+                    }
+                }
+            }
+        }
+    }
+    const uint32_t kk = p->k < TOPK_KMAX ? p->k : TOPK_KMAX;
+    for (uint32_t i = 0; i < kk; i++) {   /* :187-195 */
+        uint32_t bits;
+        memcpy(&bits, &v[i], 4);
+        result[p->out_offset + i] = bits;
+        result[p->out_offset + kk + i] = ix[i];
+    }
+    free(v);
+    free(ix);
+}

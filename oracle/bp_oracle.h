@@ -152,6 +152,19 @@ typedef struct {            /* MatmulParams, src/model.rs:182-192 */
 void bpo_matmul_q1_0_q8_0(const bpo_matmul_params* p, const uint8_t* weights, const uint8_t* acts,
                           uint16_t* y);
 
+/* ---- top-k of the logits: src/shaders/topk_reduce.wgsl -------------------- */
+typedef struct {            /* TopKParams, src/forward.rs:343-348 field order */
+    uint32_t n, in_offset, out_offset, k;
+} bpo_topk_params;
+/* The reference's single-workgroup network, restated step for step so that
+ * ties resolve to the same indices: 256 lanes, lane t owns the f16 pairs at
+ * words t, t+256, ...; per lane a 32-entry min-heap (strict > insertion,
+ * -1e30 / index 0 initial), heap sort to descending, then the pairwise
+ * bitonic tree merge (lists p and p+s, s = 128 .. 1). Writes
+ * result[out_offset + i] = f32 bits of value i and
+ * result[out_offset + kk + i] = its index, kk = min(k, 32). */
+void bpo_topk_reduce(const bpo_topk_params* p, const uint16_t* act, uint32_t* result);
+
 /* ---- seeded synthetic inputs (splitmix64 + Box-Muller) -------------------- */
 void bpo_fill_normal_f16(uint64_t seed, float mean, float stddev, uint16_t* out, size_t n);
 

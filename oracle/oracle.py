@@ -87,6 +87,11 @@ class MatmulParams(ctypes.Structure):
                                      "out_offset", "accumulate")]
 
 
+class TopKParams(ctypes.Structure):
+    """TopKParams, src/forward.rs:343-348 (n, in_offset, out_offset, k)."""
+    _fields_ = [(n, _u32) for n in ("n", "in_offset", "out_offset", "k")]
+
+
 def _sig(name, res, args):
     f = getattr(_lib, name)
     f.restype, f.argtypes = res, args
@@ -117,6 +122,7 @@ _attn = _sig("bpo_attention", None, [ctypes.POINTER(AttnParams), _vp, _vp, _vp, 
 _fill = _sig("bpo_fill_normal_f16", None, [_u64, _f32, _f32, _vp, ctypes.c_size_t])
 _quant_act = _sig("bpo_quantize_act_q8_0", None, [ctypes.POINTER(QuantParams), _vp, _vp])
 _matmul = _sig("bpo_matmul_q1_0_q8_0", None, [ctypes.POINTER(MatmulParams), _vp, _vp, _vp])
+_topk = _sig("bpo_topk_reduce", None, [ctypes.POINTER(TopKParams), _vp, _vp])
 _f16_add = _sig("bpo_f16_add", ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16])
 _f16_mul = _sig("bpo_f16_mul", ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16])
 _mv = _sig("bpo_matvec_q1_0", None, [ctypes.POINTER(MatvecParams), _vp, _vp])
@@ -300,4 +306,12 @@ def matmul_q1_0_q8_0(p: MatmulParams, weights: np.ndarray, acts: np.ndarray, y) 
     out = _u16(y).copy()
     _matmul(ctypes.byref(p), _ptr(np.ascontiguousarray(weights, np.uint8)),
             _ptr(np.ascontiguousarray(acts, np.uint8)), _ptr(out))
+    return out
+
+
+def topk_reduce(p: "TopKParams", act, result) -> np.ndarray:
+    """Returns a copy of result (uint32 words) with the top-k values (f32 bits,
+    descending) and their indices written at p.out_offset."""
+    out = np.ascontiguousarray(result, np.uint32).copy()
+    _topk(ctypes.byref(p), _ptr(_u16(act)), _ptr(out))
     return out

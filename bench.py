@@ -370,7 +370,7 @@ def bench_lm_head(torch, args, vocab=151936, n_copies=8):
     return {"n_k": [vocab, H], "kernel_us_avg": us, "bytes": byt, "GBps": byt / (us * 1e-6) / 1e9,
             "frac_hbm": byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "topk_reduce_k32": {"n": vocab, "us_avg": tk_us, "bytes": 2 * vocab,
-                                "note": "2 launches (per-lane heaps, merge tree); latency-bound"}}
+                                "note": "one 1024-thread workgroup, latency-bound"}}
 
 
 def bench_matmul(torch, args, m_tokens=512, n_layer=8):

@@ -40,7 +40,6 @@ struct bp_model {
     uint64_t partials_floats;
     uint16_t* kv16;       // prefill: f16 image of one layer's K and V (prefill_image_bytes)
     uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
-    void* topk_lists;     // top-k scratch: 256 sorted lists of 32 {value, index}
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
     int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 f16 sums in the reference's order, 2 i8 MFMA
@@ -274,8 +273,7 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
         hipMalloc(&m->rope_cs, rope_elems * 2) != hipSuccess ||
         hipMalloc(&m->partials, m->partials_floats * 4) != hipSuccess ||
         hipMalloc(&m->q_norm, static_cast<size_t>(cfg->n_head) * cfg->head_dim * 2) != hipSuccess ||
-        hipMalloc(&m->kv16, bp::prefill_image_bytes(cfg->n_kv_head, max_seq)) != hipSuccess ||
-        hipMalloc(&m->topk_lists, bp::topk_scratch_bytes()) != hipSuccess) {
+        hipMalloc(&m->kv16, bp::prefill_image_bytes(cfg->n_kv_head, max_seq)) != hipSuccess) {
         (void)hipGetLastError();
         return bail(fail(BP_ERR_OUT_OF_MEMORY, "hipMalloc failed for KV cache of %llu bytes x2",
                          static_cast<unsigned long long>(m->kv_bytes)));
@@ -301,7 +299,6 @@ void bp_model_destroy(bp_model* m) {
         if (m->partials) (void)hipFree(m->partials);
         if (m->kv16) (void)hipFree(m->kv16);
         if (m->q_norm) (void)hipFree(m->q_norm);
-        if (m->topk_lists) (void)hipFree(m->topk_lists);
     }
     (void)hipGetLastError();
     delete m;
@@ -640,7 +637,6 @@ bp_status bp_dispatch_topk_reduce(bp_model* m, const void* act, void* result, ui
     bp::TopKArgs a{};
     a.logits = static_cast<const uint16_t*>(act);
     a.result = static_cast<uint32_t*>(result);
-    a.lists = static_cast<uint2*>(m->topk_lists);
     a.n = n;
     a.in_offset = in_off;
     a.out_offset = out_off;

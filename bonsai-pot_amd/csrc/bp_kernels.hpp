@@ -142,10 +142,8 @@ struct MatmulArgs {
 struct TopKArgs {
     const uint16_t* logits;   // f16 activation buffer
     uint32_t* result;         // u32 result buffer
-    uint2* lists;             // scratch: 256 sorted lists of 32 {f32 bits, index}
     uint32_t n, in_offset, out_offset, k;   // in_offset: f16 elements (rounded down to even)
 };
-uint64_t topk_scratch_bytes();
 hipError_t launch_topk_reduce(const TopKArgs& a, hipStream_t s);
 hipError_t launch_quantize_act_q8_0(const QuantArgs& a, hipStream_t s);
 hipError_t launch_matmul_q1_0_q8_0(const MatmulArgs& a, hipStream_t s);

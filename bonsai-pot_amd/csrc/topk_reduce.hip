@@ -6,31 +6,56 @@
 // entries start at -1e30 / index 0), heap-sorts it to descending order, and
 // the 256 lists are then merged pairwise (list p absorbs list p + s for s =
 // 128, 64, .., 1) by one compare stage against the reversed partner and a
-// 5-stage bitonic sort. Which of several equal logits survives depends on
-// exactly that sequence of heap and network steps, so both are kept; what
-// changes is where they run:
+// 5-stage bitonic sort. Which of several equal logits survives, and in which
+// order, follows from that exact sequence of steps.
 //
-//  * topk_lane_kernel: one wave per reference thread t (256 waves, one per
-//    CU). The heap lives in lanes 0..31 of two VGPRs (value, index); a sift
-//    is a chain of uniform-index readlane steps and lane-selects, so nothing goes
-//    through LDS. The wave loads 64 of its words at a time (64 elements x 2),
-//    and a ballot of "v > heap minimum, at or after the cursor" finds the next
-//    element that the reference's loop would insert; the rejected elements
-//    cost nothing beyond that one compare. Each wave writes its sorted list
-//    (32 x {value, index}) to the scratch buffer.
-//  * topk_merge_kernel: one 1024-thread workgroup runs the 8 merge levels on
-//    the 256 lists in LDS. One merge is one wave: list p in lanes 0..31, list
-//    p + s in lanes 32..63; the compare against the reversed partner is one
-//    lane permute (lane i reads lane 63 - i), the bitonic stages are xor
-//    shuffles of stride 16 .. 1 with the reference's strict compare-swap.
+// This kernel gets the same result without running 256 sequential heaps. Call
+// an element "big" if its value is >= V, the 32nd-largest insertable value
+// (insertable: > -1e30, i.e. not NaN and not -inf), and every other list
+// entry "small". Every compare of the heaps and of the merge network between a
+// big and a small is decided by the values alone, and compares between smalls
+// only move smalls among the slots that smalls occupy. So the final top 32 (all
+// bigs) do not depend on the smalls' values or order, only on which list slots
+// hold smalls. In a reference thread whose bigs have pairwise different values,
+// the heap-sorted list holds those bigs in descending order in its first slots
+// and smalls in the rest; that list can be written directly, with -1e30 /
+// index 0 as the smalls. Only threads with two equal bigs need their heap
+// replayed step by step.
+//
+// One 1024-thread workgroup:
+//  1. every thread takes the maximum of its share of the logits (16-byte
+//     loads); tau = the 32nd largest of these 1024 maxima, by a two-round
+//     radix select on 16-bit order keys (so at least 32 elements are >= tau);
+//  2. the elements >= tau (a few dozen on real logits) are gathered in LDS
+//     (16-byte groups whose maximum, kept in LDS by step 1, is below tau are
+//     skipped); among them V (exact) and the bigs follow by counting, and each
+//     big's slot in its reference thread's list by counting the larger bigs of
+//     that thread (one wave when there are at most 64); equal bigs in one
+//     thread mark it "replay";
+//  3. the replayed threads run the reference heap, one wave per thread (heap
+//     in lanes 0..31, sifts by uniform readlanes), reading the logits again;
+//     more than kCap gathered elements (massive ties) replay all 256;
+//  4. the merge tree on the 256 lists in LDS, one merge per wave: list p in
+//     lanes 0..31, list p + s in lanes 32..63, the reversed compare one lane
+//     permute, the bitonic stages lane exchanges (DPP for strides 1-8) with
+//     the reference's strict compare-swap; merges whose second list is pure
+//     fill are skipped (lists are sorted descending, so they are no-ops).
+#include <climits>
+
 #include "bp_device.hpp"
 #include "bp_kernels.hpp"
 
 namespace bp {
 namespace {
 
-constexpr uint32_t kLanes = 256;   // reference workgroup size
-constexpr uint32_t kK = 32;        // K_MAX
+constexpr uint32_t kLanes = 256;    // reference workgroup size
+constexpr uint32_t kK = 32;         // K_MAX
+constexpr uint32_t kThreads = 1024;
+constexpr uint32_t kWaves = kThreads / 64;
+constexpr uint32_t kCap = 2048;     // gathered elements >= tau
+constexpr uint32_t kRegGroups = 19; // 16-byte groups per thread loaded together
+constexpr uint32_t kGmaxCap = kRegGroups * 1024;   // group maxima kept in LDS
+constexpr float kEmpty = -1e30f;    // the reference's initial heap value
 
 __device__ __forceinline__ float rl(float v, uint32_t lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -39,9 +64,7 @@ __device__ __forceinline__ uint32_t rl(uint32_t v, uint32_t lane) {
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
 }
 // writelane: `x` in lane `lane` (uniform), `old` elsewhere
-__device__ __forceinline__ float wl(float x, uint32_t lane, float old) {
-    return __lane_id() == lane ? x : old;
-}
+__device__ __forceinline__ float wl(float x, uint32_t lane, float old) { return __lane_id() == lane ? x : old; }
 __device__ __forceinline__ uint32_t wl(uint32_t x, uint32_t lane, uint32_t old) {
     return __lane_id() == lane ? x : old;
 }
@@ -50,7 +73,7 @@ __device__ __forceinline__ uint32_t wl(uint32_t x, uint32_t lane, uint32_t old) 
 // wins ties; a strictly smaller child moves up), topk_reduce.wgsl:42-55.
 __device__ __forceinline__ void sift(float& hv, uint32_t& hi, uint32_t len) {
     uint32_t i = 0;
-    float vi = rl(hv, 0);
+    const float vi = rl(hv, 0);
     for (;;) {
         const uint32_t l = 2 * i + 1, r = l + 1;
         uint32_t m = i;
@@ -69,23 +92,23 @@ __device__ __forceinline__ void sift(float& hv, uint32_t& hi, uint32_t len) {
         hv = wl(vi, m, hv);
         hi = wl(im, i, hi);
         hi = wl(ii, m, hi);
-        i = m;   // vi (the sifted value) is unchanged
+        i = m;   // the sifted value vi moves down with i
     }
 }
 
-__global__ __launch_bounds__(64) void topk_lane_kernel(TopKArgs a) {
-    const uint32_t t = blockIdx.x;   // reference thread
-    const uint32_t lane = threadIdx.x;
-    const uint32_t* words = reinterpret_cast<const uint32_t*>(a.logits + (a.in_offset & ~1u));
-    const uint32_t n_words = (a.n + 1) / 2;
-    float hv = -1e30f;
-    uint32_t hi = 0;
-    float root = -1e30f;
-    // words t + 256 (64 c + lane), chunk c
+// The reference thread t's heap (topk_reduce.wgsl:65-115), replayed by one
+// wave: lanes 0..31 end with its list, descending.
+__device__ void replay_thread(const uint32_t* words, uint32_t n, uint32_t t, float& hv, uint32_t& hi) {
+    const uint32_t lane = __lane_id();
+    const uint32_t n_words = (n + 1) / 2;
+    hv = kEmpty;
+    hi = 0;
+    float root = kEmpty;
+    // words t + 256 (64 c + lane) for chunk c, visited in order
     for (uint32_t base = t; base < n_words; base += kLanes * 64) {
         const uint32_t w = base + kLanes * lane;
         const bool ok0 = w < n_words;
-        const bool ok1 = ok0 && 2 * w + 1 < a.n;
+        const bool ok1 = ok0 && 2 * w + 1 < n;
         const uint32_t pair = ok0 ? words[w] : 0u;
         const float v0 = h2f(static_cast<uint16_t>(pair & 0xFFFFu));
         const float v1 = h2f(static_cast<uint16_t>(pair >> 16));
@@ -106,8 +129,7 @@ __global__ __launch_bounds__(64) void topk_lane_kernel(TopKArgs a) {
             cursor = 2 * j + h + 1;
         }
     }
-    // heap sort to descending (topk_reduce.wgsl:98-115)
-    for (uint32_t last = kK - 1; last > 0; last--) {
+    for (uint32_t last = kK - 1; last > 0; last--) {   // heap sort, :98-115
         const float v0 = rl(hv, 0), vl = rl(hv, last);
         const uint32_t i0 = rl(hi, 0), il = rl(hi, last);
         hv = wl(vl, 0, hv);
@@ -116,42 +138,357 @@ __global__ __launch_bounds__(64) void topk_lane_kernel(TopKArgs a) {
         hi = wl(i0, last, hi);
         sift(hv, hi, last);
     }
-    if (lane < kK) a.lists[t * kK + lane] = make_uint2(__builtin_bit_cast(uint32_t, hv), hi);
 }
 
-// One strict compare-swap stage of stride s across lanes (lane ^ s).
-__device__ __forceinline__ void cswap(float& v, uint32_t& ix, uint32_t lane, int s) {
-    const float pv = __shfl_xor(v, s);
-    const uint32_t pi = __shfl_xor(ix, s);
-    const bool lo = (lane & s) == 0;
-    // reference: if v[hi] > v[lo] swap
-    const bool take = lo ? (pv > v) : (v > pv);
-    if (take) { v = pv; ix = pi; }
+// Value of lane (lane ^ S): DPP lane moves for S = 1, 2, 4, 8 (quad
+// permutes, half-row mirror + quad permute, row rotation by 8), a permute
+// through the LDS crossbar for 16.
+template <int S>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    const int x = static_cast<int>(v);
+    if constexpr (S == 1) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    else if constexpr (S == 2) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    else if constexpr (S == 4) {
+        const int m = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);   // lane ^ 7
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false));   // ^ 3
+    } else if constexpr (S == 8) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    else return static_cast<uint32_t>(__shfl_xor(x, S));
 }
 
-__global__ __launch_bounds__(1024) void topk_merge_kernel(TopKArgs a) {
-    __shared__ uint2 lists[kLanes * kK];   // 64 KB
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (uint32_t i = tid; i < kLanes * kK; i += 1024) lists[i] = a.lists[i];
-    __syncthreads();
-    for (uint32_t s = kLanes / 2; s > 0; s /= 2) {
-        for (uint32_t p = wave; p < s; p += 16) {
-            const uint2 x = lists[(lane < kK ? p : p + s) * kK + (lane & (kK - 1))];
-            float v = __builtin_bit_cast(float, x.x);
-            uint32_t ix = x.y;
-            // stage 0: a[i] = b[31 - i] if strictly greater (b[31 - i] sits in lane 63 - i)
-            const float bv = __shfl(v, 63 - lane);
-            const uint32_t bi = __shfl(ix, 63 - lane);
-            if (bv > v) { v = bv; ix = bi; }
+// One strict compare-swap stage of stride S (lanes l, l ^ S) on two lists.
+template <int S>
+__device__ __forceinline__ void merge_stages(float (&v)[2], uint32_t (&ix)[2], uint32_t lane) {
+    const bool lo = (lane & S) == 0;
 #pragma unroll
-            for (int st = kK / 2; st >= 1; st >>= 1) cswap(v, ix, lane, st);
-            if (s > 1) {
-                if (lane < kK) lists[p * kK + lane] = make_uint2(__builtin_bit_cast(uint32_t, v), ix);
-            } else {
-                const uint32_t kk = a.k < kK ? a.k : kK;
-                if (lane < kk) {
-                    a.result[a.out_offset + lane] = __builtin_bit_cast(uint32_t, v);
-                    a.result[a.out_offset + kk + lane] = ix;
+    for (int u = 0; u < 2; u++) {
+        const float pv = __builtin_bit_cast(float, xor_lane<S>(__builtin_bit_cast(uint32_t, v[u])));
+        const uint32_t pi = xor_lane<S>(ix[u]);
+        const bool take = lo ? (pv > v[u]) : (v[u] > pv);   // reference: if v[hi] > v[lo] swap
+        v[u] = take ? pv : v[u];
+        ix[u] = take ? pi : ix[u];
+    }
+}
+
+// 16-bit key with the order of the f16 values (-0 and +0 share a key).
+__device__ __forceinline__ uint32_t hkey(uint16_t h) {
+    if (h == 0x8000u) h = 0;
+    return (h & 0x8000u) ? (~h & 0xFFFFu) : (h | 0x8000u);
+}
+__device__ __forceinline__ uint16_t unkey16(uint32_t k) {   // inverse of hkey (+0 for key 0x8000)
+    return static_cast<uint16_t>((k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu));
+}
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+// Packed maximum of the 8 f16 values of a 16-byte group (as 2 lanes).
+__device__ __forceinline__ h2 group_max(const uint4& q) {
+    const h2 a = __builtin_elementwise_max(__builtin_bit_cast(h2, q.x), __builtin_bit_cast(h2, q.y));
+    const h2 b = __builtin_elementwise_max(__builtin_bit_cast(h2, q.z), __builtin_bit_cast(h2, q.w));
+    return __builtin_elementwise_max(a, b);
+}
+__device__ __forceinline__ bool insertable(uint16_t h) {   // > -1e30 as f32: not NaN, not -inf
+    return (h & 0x7FFFu) <= 0x7C00u && h != 0xFC00u;
+}
+
+struct TopKShared {
+    uint2 lists[kLanes * kK];   // {f32 bits, index}
+    uint32_t hist[256];
+    _Float16 gmax[kGmaxCap];    // maximum of each 16-byte group (maxNum: NaN-free unless all NaN)
+    uint2 cand[kCap];
+    uint32_t cand_big[kCap];    // 1 if a big
+    uint32_t cand_slot[kCap];   // a big's slot in its thread's list
+    uint32_t replay[kLanes];    // per reference thread: 1 = replay its heap
+    uint32_t replay_ids[kLanes];
+    uint32_t dirty[kLanes];     // list holds anything but the -1e30 / 0 fill
+    uint32_t n_cand, n_replay, sel_hi, sel_rank, tau_key;
+};
+
+// Key of the rank-th largest (0-based) of the 1024 keys held one per thread
+// (0 = no value), by two 8-bit radix rounds; 0 if fewer than rank + 1 keys.
+__device__ uint32_t select_key(TopKShared& sh, uint32_t key, uint32_t rank) {
+    const uint32_t tid = threadIdx.x;
+    for (int round = 0; round < 2; round++) {
+        if (tid < 256) sh.hist[tid] = 0;
+        __syncthreads();
+        const bool in = key != 0 && (round == 0 || (key >> 8) == sh.sel_hi);
+        const uint32_t bin = round == 0 ? key >> 8 : key & 0xFFu;
+        // one atomic per distinct bin of the wave (the keys crowd into few bins)
+        uint64_t left = __ballot(in);
+        while (left) {
+            const uint32_t b = __builtin_amdgcn_readlane(bin, __builtin_ctzll(left));
+            const uint64_t same = __ballot(in && bin == b) & left;
+            if ((threadIdx.x & 63) == __builtin_ctzll(same)) atomicAdd(&sh.hist[b], static_cast<uint32_t>(__popcll(same)));
+            left &= ~same;
+        }
+        __syncthreads();
+        if (tid < 64) {   // one wave scans the bins from the top
+            const uint32_t want = round == 0 ? rank : sh.sel_rank;
+            uint32_t c[4], tot = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) { c[i] = sh.hist[255 - (4 * tid + i)]; tot += c[i]; }
+            uint32_t incl = tot;   // inclusive prefix over lanes (bins from the top)
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = __shfl_up(incl, off);
+                if (tid >= static_cast<uint32_t>(off)) incl += o;
+            }
+            uint32_t run = incl - tot;
+            bool found = false;
+            uint32_t bin = 0, above = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (!found && run + c[i] > want) { found = true; bin = 255 - (4 * tid + i); above = run; }
+                run += c[i];
+            }
+            const uint64_t fm = __ballot(found);
+            if (fm == 0) {
+                if (tid == 0) { sh.sel_hi = 0xFFFFFFFFu; sh.tau_key = 0; }
+            } else if (tid == __builtin_ctzll(fm)) {
+                if (round == 0) { sh.sel_hi = bin; sh.sel_rank = want - above; }
+                else sh.tau_key = (sh.sel_hi << 8) | bin;
+            }
+        }
+        __syncthreads();
+        if (sh.sel_hi == 0xFFFFFFFFu) return 0;
+    }
+    return sh.tau_key;
+}
+
+__global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
+    __shared__ TopKShared sh;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint16_t* x = a.logits + (a.in_offset & ~1u);
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(x);
+    const uint32_t n = a.n;
+    // 16-byte groups of 8 elements from the first 16-byte boundary; the
+    // elements before it (head, < 8) and after the last group (tail) are
+    // visited one by one.
+    const uint32_t head = min(static_cast<uint32_t>(((16u - (reinterpret_cast<uintptr_t>(x) & 15u)) & 15u) / 2u), n);
+    const uint32_t n_groups = (n - head) / 8;
+    const uint32_t tail0 = head + 8 * n_groups;
+    const uint4* groups = reinterpret_cast<const uint4*>(x + head);
+    auto single = [&](uint32_t i) -> uint16_t { return i < n ? x[i] : static_cast<uint16_t>(0xFC00u); };
+
+    if (tid == 0) { sh.n_cand = 0; sh.n_replay = 0; }
+    for (uint32_t i = tid; i < kLanes * kK; i += kThreads)
+        sh.lists[i] = make_uint2(__builtin_bit_cast(uint32_t, kEmpty), 0u);
+    if (tid < kLanes) { sh.replay[tid] = 0; sh.dirty[tid] = 0; }
+
+    // ---- 1. per-thread maximum key of the insertable values. The groups are
+    // taken kRegGroups per thread at a time into registers (all loads in
+    // flight together); with n up to kRegGroups * 8192 the gather below reuses
+    // them instead of reading again.
+    const uint32_t per_round = kRegGroups * kThreads;
+    const uint32_t n_rounds = (n_groups + per_round - 1) / per_round;
+    uint4 q[kRegGroups];
+    auto load_round = [&](uint32_t r) __attribute__((always_inline)) {
+        // unconditional loads of clamped groups (n_groups >= 1 here), so that
+        // all of them are in flight before the first is used
+#pragma unroll
+        for (uint32_t u = 0; u < kRegGroups; u++) {
+            const uint32_t g = r * per_round + u * kThreads + tid;
+            q[u] = groups[min(g, n_groups - 1)];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kRegGroups; u++) {
+            const uint32_t g = r * per_round + u * kThreads + tid;
+            if (g >= n_groups) q[u] = make_uint4(0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u);
+        }
+    };
+    // packed f16 maximum (maxNum: NaN operands drop out; -inf is the identity)
+    h2 hm = {-INFINITY, -INFINITY};
+    for (uint32_t r = 0; r < n_rounds; r++) {
+        load_round(r);
+#pragma unroll
+        for (uint32_t u = 0; u < kRegGroups; u++) {
+            const h2 gm = group_max(q[u]);
+            hm = __builtin_elementwise_max(hm, gm);
+            const uint32_t g = r * per_round + u * kThreads + tid;
+            const _Float16 g0 = gm.x, g1 = gm.y;   // (scalars before the cast)
+            if (g < kGmaxCap) sh.gmax[g] = g0 > g1 ? g0 : g1;
+        }
+    }
+    uint32_t mk = 0;
+    auto take_max = [&](uint16_t h) { if (insertable(h)) mk = max(mk, hkey(h)); };
+    {   // copied to scalars before the bit casts (a bit cast of a vector element
+        // directly compiles to element 0)
+        const _Float16 m0 = hm.x, m1 = hm.y;
+        take_max(__builtin_bit_cast(uint16_t, m0));
+        take_max(__builtin_bit_cast(uint16_t, m1));
+    }
+    if (tid < 8) take_max(single(tid < head ? tid : n));
+    else if (tid < 16) take_max(single(tail0 + tid - 8));
+    // tau: the 32nd largest maximum (at least 32 elements are >= tau); with
+    // fewer than 32 maxima, every insertable element is gathered
+    uint32_t tau = select_key(sh, mk, kK - 1);
+    if (tau == 0) tau = hkey(0xFBFFu);   // -65504, the smallest insertable value
+    const float tau_f = h2f(unkey16(tau));
+
+    // ---- 2. gather the elements >= tau (few on real logits): one LDS atomic
+    // per 8-element group that holds any; past kCap every heap is replayed
+    auto take = [&](uint16_t h) { return insertable(h) && hkey(h) >= tau; };
+    // groups whose maximum reaches tau (maxima from LDS up to kGmaxCap groups,
+    // recomputed beyond), then their elements
+#pragma unroll 1
+    for (uint32_t g = tid; g < n_groups; g += kThreads) {
+        float gmf;
+        if (g < kGmaxCap) {
+            gmf = static_cast<float>(sh.gmax[g]);
+        } else {
+            const h2 gm = group_max(groups[g]);
+            const _Float16 g0 = gm.x, g1 = gm.y;
+            gmf = fmaxf(static_cast<float>(g0), static_cast<float>(g1));
+        }
+        if (!(gmf >= tau_f)) continue;
+        const uint4 qg = groups[g];
+        const uint32_t w[4] = {qg.x, qg.y, qg.z, qg.w};
+        uint32_t m = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) m |= take(static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)))) ? 1u << e : 0u;
+        uint32_t slot = atomicAdd(&sh.n_cand, static_cast<uint32_t>(__popc(m)));
+#pragma unroll 1
+        for (; m; m &= m - 1, slot++) {
+            const int e = __builtin_ctz(m);
+            const uint16_t h = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+            if (slot < kCap) sh.cand[slot] = make_uint2(__builtin_bit_cast(uint32_t, h2f(h)), head + 8 * g + e);
+        }
+    }
+    if (wave == 0) {   // head and tail elements
+        const uint32_t i = lane < 8 ? lane : tail0 + lane - 8;
+        const bool ok = lane < 8 ? lane < head : (lane < 16 && i < n);
+        if (ok && take(x[i])) {
+            const uint32_t slot = atomicAdd(&sh.n_cand, 1u);
+            if (slot < kCap) sh.cand[slot] = make_uint2(__builtin_bit_cast(uint32_t, h2f(x[i])), i);
+        }
+    }
+    __syncthreads();
+    const uint32_t n_cand = sh.n_cand;
+    const bool overflow = n_cand > kCap;
+    if (!overflow && n_cand <= 64) {
+        // one wave: lane i holds candidate i; the others' values by readlane
+        if (wave == 0) {
+            const bool live = lane < n_cand;
+            const uint2 c = live ? sh.cand[lane] : make_uint2(__builtin_bit_cast(uint32_t, kEmpty), 0u);
+            const float vi = __builtin_bit_cast(float, c.x);
+            const uint32_t ti = (c.y >> 1) & (kLanes - 1);
+            uint32_t g = 0;
+            for (uint32_t j = 0; j < n_cand; j++) g += rl(vi, j) > vi;
+            const bool big = live && g < kK;
+            const uint64_t bigm = __ballot(big);
+            uint32_t r = 0;
+            bool dup = false;
+            for (uint32_t j = 0; j < n_cand; j++) {
+                if (!((bigm >> j) & 1u)) continue;
+                const float vj = rl(vi, j);
+                const uint32_t tj = rl(ti, j);
+                if (j == lane || tj != ti) continue;
+                r += vj > vi;
+                dup = dup || vj == vi;
+            }
+            if (big && (dup || r >= kK)) sh.replay[ti] = 1;
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_wave_barrier();
+            if (big && r < kK && !sh.replay[ti]) { sh.lists[ti * kK + r] = c; sh.dirty[ti] = 1; }
+        }
+        __syncthreads();   // the replay flags are read by waves 0-3 below
+    } else if (!overflow) {
+        // V = the 32nd largest gathered value; bigs = gathered values >= V,
+        // i.e. fewer than 32 gathered values above them
+        for (uint32_t i = tid; i < n_cand; i += kThreads) {
+            const float vi = __builtin_bit_cast(float, sh.cand[i].x);
+            uint32_t g = 0;
+            for (uint32_t j = 0; j < n_cand; j++) g += __builtin_bit_cast(float, sh.cand[j].x) > vi;
+            sh.cand_big[i] = g < kK ? 1u : 0u;
+        }
+        __syncthreads();
+        // slot of each big in its reference thread's list; equal bigs -> replay
+        for (uint32_t i = tid; i < n_cand; i += kThreads) {
+            if (!sh.cand_big[i]) continue;
+            const float vi = __builtin_bit_cast(float, sh.cand[i].x);
+            const uint32_t ti = (sh.cand[i].y >> 1) & (kLanes - 1);
+            uint32_t r = 0;
+            bool dup = false;
+            for (uint32_t j = 0; j < n_cand; j++) {
+                if (j == i || !sh.cand_big[j]) continue;
+                if (((sh.cand[j].y >> 1) & (kLanes - 1)) != ti) continue;
+                const float vj = __builtin_bit_cast(float, sh.cand[j].x);
+                r += vj > vi;
+                dup = dup || vj == vi;
+            }
+            if (dup || r >= kK) sh.replay[ti] = 1;
+            sh.cand_slot[i] = r;
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < n_cand; i += kThreads) {
+            if (!sh.cand_big[i]) continue;
+            const uint32_t r = sh.cand_slot[i];
+            const uint32_t ti = (sh.cand[i].y >> 1) & (kLanes - 1);
+            if (r < kK && !sh.replay[ti]) { sh.lists[ti * kK + r] = sh.cand[i]; sh.dirty[ti] = 1; }
+        }
+    }
+    if (tid < kLanes && (overflow || sh.replay[tid])) sh.replay_ids[atomicAdd(&sh.n_replay, 1u)] = tid;
+    __syncthreads();
+
+    // ---- 3. replay the reference heaps that the shortcut cannot write
+    const uint32_t n_replay = sh.n_replay;
+    for (uint32_t e = wave; e < n_replay; e += kWaves) {
+        const uint32_t t = sh.replay_ids[e];
+        float hv;
+        uint32_t hi;
+        replay_thread(words, n, t, hv, hi);
+        if (lane < kK) sh.lists[t * kK + lane] = make_uint2(__builtin_bit_cast(uint32_t, hv), hi);
+        if (lane == 0) sh.dirty[t] = 1;
+    }
+    __syncthreads();
+
+    // ---- 4. merge tree (topk_reduce.wgsl:117-184). Lists are always sorted
+    // descending, so a merge whose second list is pure fill (-1e30 / 0, which
+    // never wins the strict compares) leaves the first one unchanged and is
+    // skipped. A wave runs its merges of a level (up to 8) side by side so that
+    // their lane-exchange chains overlap.
+#pragma unroll 1
+    for (uint32_t s = kLanes / 2; s > 0; s /= 2) {
+        uint32_t need = 0;   // bit u: merge p = wave + 16 u runs
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t p = wave + kWaves * u;
+            if (p < s && (s == 1 || sh.dirty[p + s])) need |= 1u << u;
+        }
+        need = __builtin_amdgcn_readfirstlane(need);   // uniform: p depends on the wave only
+#pragma unroll 1
+        for (int u0 = 0; u0 < 8; u0 += 2) {
+            const uint32_t nd = (need >> u0) & 3u;
+            if (!nd) continue;
+            float v[2];
+            uint32_t ix[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t p = wave + kWaves * (u0 + u);
+                const uint2 xv = (nd >> u) & 1u ? sh.lists[(lane < kK ? p : p + s) * kK + (lane & (kK - 1))]
+                                                : make_uint2(__builtin_bit_cast(uint32_t, kEmpty), 0u);
+                // stage 0: a[i] = b[31 - i] if strictly greater (b[31 - i] sits in lane 63 - i)
+                v[u] = __builtin_bit_cast(float, xv.x);
+                ix[u] = xv.y;
+                const float bv = __shfl(v[u], 63 - lane);
+                const uint32_t bi = __shfl(ix[u], 63 - lane);
+                if (bv > v[u]) { v[u] = bv; ix[u] = bi; }
+            }
+            merge_stages<16>(v, ix, lane);
+            merge_stages<8>(v, ix, lane);
+            merge_stages<4>(v, ix, lane);
+            merge_stages<2>(v, ix, lane);
+            merge_stages<1>(v, ix, lane);
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                if (!((nd >> u) & 1u)) continue;
+                const uint32_t p = wave + kWaves * (u0 + u);
+                if (s > 1) {
+                    if (lane < kK) sh.lists[p * kK + lane] = make_uint2(__builtin_bit_cast(uint32_t, v[u]), ix[u]);
+                    if (lane == 0) sh.dirty[p] = 1;
+                } else {
+                    const uint32_t kk = a.k < kK ? a.k : kK;
+                    if (lane < kk) {
+                        a.result[a.out_offset + lane] = __builtin_bit_cast(uint32_t, v[u]);
+                        a.result[a.out_offset + kk + lane] = ix[u];
+                    }
                 }
             }
         }
@@ -161,11 +498,8 @@ __global__ __launch_bounds__(1024) void topk_merge_kernel(TopKArgs a) {
 
 }  // namespace
 
-uint64_t topk_scratch_bytes() { return static_cast<uint64_t>(kLanes) * kK * sizeof(uint2); }
-
 hipError_t launch_topk_reduce(const TopKArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(topk_lane_kernel, dim3(kLanes), dim3(64), 0, s, a);
-    hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL(topk_kernel, dim3(1), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

@@ -130,6 +130,30 @@ def _cases():
     for n in (0, 1, 3, 31, 33, 511, 512, 513, 16385):
         yield f"small_{n}", rng.integers(-4, 4, n + 4).astype(np.float16), 32, 4
     yield "k40_clamped", (rng.standard_normal(VOCAB)).astype(np.float16), 40, 0
+    # ties among the top values inside one reference thread (words t, t+256, ..)
+    x = (rng.standard_normal(VOCAB) * 2).astype(np.float16)
+    a = int(rng.integers(0, VOCAB // 2)) & ~1
+    for d in (0, 1, 512, 1024 * 7 + 1):           # same thread: (i >> 1) % 256 equal
+        x[a + d] = 12.5
+    x[a + 3] = 12.5                                 # another thread, same value
+    yield "thread_tie", x, 32, 0
+    x = (rng.standard_normal(VOCAB) * 2).astype(np.float16)
+    x[rng.choice(VOCAB, 40, replace=False)] = 11.0  # ties spread over threads
+    yield "spread_tie", x, 32, 0
+    x = (rng.standard_normal(VOCAB)).astype(np.float16)
+    x[rng.choice(VOCAB, 1500, replace=False)] = 9.0  # many gathered, under the cap
+    yield "near_cap", x, 32, 0
+    x = (rng.standard_normal(VOCAB)).astype(np.float16)
+    x[rng.choice(VOCAB, 2100, replace=False)] = 9.0  # over the cap: every heap replayed
+    yield "over_cap", x, 32, 0
+    x = np.full(VOCAB, -np.inf, np.float16)
+    x[rng.choice(VOCAB, 20, replace=False)] = rng.standard_normal(20)
+    yield "few_finite", x, 32, 0
+    x = -np.abs(rng.standard_normal(VOCAB)).astype(np.float16) - np.float16(1)
+    z = rng.choice(VOCAB, 60, replace=False)
+    x[z[:30]] = 0.0
+    x[z[30:]] = -0.0
+    yield "signed_zeros", x, 32, 0
 
 
 @pytest.mark.gpu

@@ -16,6 +16,10 @@ LIB = os.path.join(HERE, "lib", "libbonsai_pot_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 SOURCES = ["bp_api.cpp", "norm_rope_writeback.hip", "attn_decode.hip", "attn_prefill.hip", "matvec_q1_0.hip", "matvec_q1_0_mfma.hip", "matmul_q1_0_q8_0.hip", "topk_reduce.hip"]
+# Per-source additions: the matmul's MFMA results go straight to VGPRs (the
+# default AGPR form costs one v_accvgpr_read per result element in its f32
+# epilogue).
+EXTRA_FLAGS = {"matmul_q1_0_q8_0.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 FLAGS = [
     "-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-Wall", "-Wno-unused-function",
@@ -38,7 +42,7 @@ def build(verbose: bool = False) -> str:
     jobs = []
     for src in SOURCES:
         obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
-        jobs.append((obj, [HIPCC, *FLAGS, "-c", "-o", obj, os.path.join(CSRC, src)]))
+        jobs.append((obj, [HIPCC, *FLAGS, *EXTRA_FLAGS.get(src, []), "-c", "-o", obj, os.path.join(CSRC, src)]))
     with ThreadPoolExecutor(max_workers=min(4, len(jobs))) as ex:
         list(ex.map(lambda j: _run(j[1]), jobs))
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB, *[o for o, _ in jobs]])

@@ -609,7 +609,7 @@ bp_status bp_dispatch_matmul_q1_0(bp_model* m, const void* weights, const void* 
         return fail(BP_ERR_INVALID_ARG, "matmul offsets: w_d 2-byte, w_qs / a_d / a_qs 4-byte aligned (%u, %u, %u, %u)",
                     w_d, w_qs, a_d, a_qs);
     if (n == 0 || n_tokens == 0) return BP_OK;
-    if ((n_tokens + 63) / 64 > 65535) return fail(BP_ERR_INVALID_ARG, "matmul: %u tokens too many", n_tokens);
+    if ((n_tokens + 31) / 32 > 65535) return fail(BP_ERR_INVALID_ARG, "matmul: %u tokens too many", n_tokens);
     bp::MatmulArgs a{};
     a.weights = static_cast<const uint8_t*>(weights);
     a.acts = static_cast<const uint8_t*>(acts_q8);

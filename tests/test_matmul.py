@@ -169,15 +169,16 @@ def _model():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("m,k", [(1, 32), (7, 2560), (64, 4096), (512, 2560), (100, 9728)])
-def test_quantize_bit_exact(cuda, m, k):
-    _say(f"[quantize] m={m} k={k}")
+@pytest.mark.parametrize("m,k,in_off,shift", [(1, 32, 24, 0), (7, 2560, 24, 0), (64, 4096, 24, 0), (512, 2560, 24, 0),
+                                              (100, 9728, 24, 0), (33, 2560, 5, 4), (9, 4096, 2, 8)])
+def test_quantize_bit_exact(cuda, m, k, in_off, shift):
+    _say(f"[quantize] m={m} k={k} in_off={in_off} shift={shift}")
     rng = np.random.default_rng(m * 7 + k)
     x = (rng.standard_normal(m * k) * np.exp(rng.standard_normal(m * k))).astype(np.float16)
     x[: min(64, x.size)] = 0                      # zero blocks
-    in_off = 24
     act = np.concatenate([_f16(rng.standard_normal(in_off)), _f16(x)])
     d_off, qs_off, size = _q8_layout(m, k)
+    d_off, qs_off, size = d_off + shift, qs_off + shift, size + shift   # unaligned to 16 bytes
     q8 = rng.integers(0, 256, size + 256, dtype=np.uint8)
     want = orc.quantize_act_q8_0(orc.QuantParams(k=k, m=m, input_offset=in_off, d_offset=d_off, qs_offset=qs_off),
                                  act, q8)

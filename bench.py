@@ -209,9 +209,16 @@ def bench_prefill(torch, args, m, pos):
     avg_us = per_launch_us(
         torch, b, lambda i: b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True), n)
     tflops = flops / (avg_us * 1e-6) / 1e12
+    # the chunk's two preceding dispatches: q norm + RoPE and the K/V writeback
+    # (the q buffer is renormalized in place each call; the values stay finite)
+    qn_us = per_launch_us(torch, b, lambda i: b.model.dispatch_q_norm_rope_fused(b.a, b.wp, b.q_off, 0, pos, m), n)
+    wb_us = per_launch_us(torch, b, lambda i: b.model.dispatch_kv_writeback_fused(
+        b.a, b.wp, b.k_off, b.v_off, b.cfg.head_dim, i % n_layer, pos, m), n)
     b.model.close()
     return {"m_tokens": m, "pos_base": pos, "flops": flops, "kernel_us_avg": avg_us,
-            "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS}
+            "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS,
+            "q_norm_rope_us": qn_us, "kv_writeback_us": wb_us,
+            "kv_writeback_GBps": m * 8 * (2 * 256 + 2 * 144) / (wb_us * 1e-6) / 1e9}
 
 
 def bench_copy(torch, args, nbytes=1 << 30):

@@ -53,6 +53,32 @@ __device__ __forceinline__ float max_xor32(float v) { const LanePair p = xchg32(
 __device__ __forceinline__ float sum_xor16(float v) { const LanePair p = xchg16(v); return p.a + p.b; }
 __device__ __forceinline__ float sum_xor32(float v) { const LanePair p = xchg32(v); return p.a + p.b; }
 
+// Value of lane (lane ^ S) for S = 1, 2, 4, 8 by DPP lane moves (quad
+// permutes; half-row mirror + quad permute; row rotation by 8), by a lane
+// permute through the LDS crossbar otherwise. Pure data movement, so
+// reductions keep their exact pairing order.
+template <int S>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    const int x = static_cast<int>(v);
+    if constexpr (S == 1) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    else if constexpr (S == 2) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    else if constexpr (S == 4) {
+        const int m = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);   // lane ^ 7 (half-row mirror)
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false));   // then ^ 3
+    } else if constexpr (S == 8) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    else return static_cast<uint32_t>(__shfl_xor(x, S));
+}
+template <int S>
+__device__ __forceinline__ float lane_xor(float v) {
+    return __builtin_bit_cast(float, lane_xor<S>(__builtin_bit_cast(uint32_t, v)));
+}
+// Value of lane 4 (lane / 4) + K (a quad broadcast).
+template <int K>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), K | (K << 2) | (K << 4) | (K << 6),
+                                                             0xF, 0xF, false));
+}
+
 // Sign-extend byte `i` of a packed word to float (exact).
 __device__ __forceinline__ float i8f(uint32_t w, int i) {
     return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * i)) >> 24);

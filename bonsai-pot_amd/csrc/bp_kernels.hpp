@@ -30,6 +30,7 @@ struct QNormRopeArgs {
     uint32_t pos_base;
     uint32_t q_dim;           // n_head * 128
     float eps;
+    uint32_t n_head, n_items;   // set by launch_q_norm_rope (m_tokens * n_head items)
 };
 
 struct KvWritebackArgs {
@@ -44,6 +45,7 @@ struct KvWritebackArgs {
     uint32_t pos_base;
     uint32_t kv_dim;          // n_kv_head * 128
     float eps;
+    uint32_t n_kv_head, n_pairs;   // set by launch_kv_writeback (m_tokens * n_kv_head pairs)
 };
 
 struct DecodeArgs {

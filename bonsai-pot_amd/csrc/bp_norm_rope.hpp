@@ -3,7 +3,7 @@
 // that every path produces the same bits.
 //
 // Layout: one 64-lane wavefront per 128-wide head, lane j holding the RoPE
-// pair (x[j], x[j+64]). Every f32 operation is one IEEE-rounded op in the
+// pair (x[j], x[j+64]); the lane exchanges of strides 1-8 are DPP moves. Every f32 operation is one IEEE-rounded op in the
 // order of the reference shaders (src/shaders/q_norm_rope_fused.wgsl,
 // src/shaders/kv_writeback_fused.wgsl in the reference repository): the
 // library is built with -ffp-contract=off, sqrt and divide are correctly
@@ -20,8 +20,12 @@ namespace bp {
 __device__ __forceinline__ void norm_rope_pair(float x0, float x1, float w0, float w1, float c,
                                                float s, float eps, float& o0, float& o1) {
     float sq = x0 * x0 + x1 * x1;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sq = sq + __shfl_xor(sq, off);
+    sq = sq + lane_xor<32>(sq);
+    sq = sq + lane_xor<16>(sq);
+    sq = sq + lane_xor<8>(sq);
+    sq = sq + lane_xor<4>(sq);
+    sq = sq + lane_xor<2>(sq);
+    sq = sq + lane_xor<1>(sq);
     float inv_h = 1.0f / sqrtf(sq / 128.0f + eps);
     float n0 = x0 * inv_h * w0;
     float n1 = x1 * inv_h * w1;
@@ -34,11 +38,11 @@ __device__ __forceinline__ void norm_rope_pair(float x0, float x1, float w0, flo
 __device__ __forceinline__ void quantize_store_pair(float x0, float x1, int lane, float* d_row,
                                                     int8_t* qs_row) {
     float a0 = fabsf(x0), a1 = fabsf(x1);
-#pragma unroll
-    for (int off = 1; off <= 16; off <<= 1) {
-        a0 = fmaxf(a0, __shfl_xor(a0, off));
-        a1 = fmaxf(a1, __shfl_xor(a1, off));
-    }
+    a0 = fmaxf(a0, lane_xor<1>(a0)); a1 = fmaxf(a1, lane_xor<1>(a1));
+    a0 = fmaxf(a0, lane_xor<2>(a0)); a1 = fmaxf(a1, lane_xor<2>(a1));
+    a0 = fmaxf(a0, lane_xor<4>(a0)); a1 = fmaxf(a1, lane_xor<4>(a1));
+    a0 = fmaxf(a0, lane_xor<8>(a0)); a1 = fmaxf(a1, lane_xor<8>(a1));
+    a0 = fmaxf(a0, lane_xor<16>(a0)); a1 = fmaxf(a1, lane_xor<16>(a1));
     float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
     float i0 = d0 > 0.0f ? 1.0f / d0 : 0.0f;
     float i1 = d1 > 0.0f ? 1.0f / d1 : 0.0f;
@@ -46,8 +50,7 @@ __device__ __forceinline__ void quantize_store_pair(float x0, float x1, int lane
     int q1 = static_cast<int>(fminf(fmaxf(rintf(x1 * i1), -127.0f), 127.0f));
     // Gather 4 consecutive lanes' bytes into one little-endian word.
     uint32_t p = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8);
-    int b = lane & ~3;
-    uint32_t p0 = __shfl(p, b), p1 = __shfl(p, b + 1), p2 = __shfl(p, b + 2), p3 = __shfl(p, b + 3);
+    const uint32_t p0 = quad_bcast<0>(p), p1 = quad_bcast<1>(p), p2 = quad_bcast<2>(p), p3 = quad_bcast<3>(p);
     if ((lane & 3) == 0) {
         uint32_t lo = (p0 & 0xffu) | ((p1 & 0xffu) << 8) | ((p2 & 0xffu) << 16) | ((p3 & 0xffu) << 24);
         uint32_t hi = (p0 >> 8) | ((p1 >> 8) << 8) | ((p2 >> 8) << 16) | ((p3 >> 8) << 24);

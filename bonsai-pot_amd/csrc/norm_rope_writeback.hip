@@ -2,8 +2,8 @@
 //
 // Restates src/shaders/q_norm_rope_fused.wgsl and
 // src/shaders/kv_writeback_fused.wgsl (reference repository) with a
-// wave64-native layout: ONE wavefront per (head, token), lane j holding the
-// RoPE pair (x[j], x[j+64]). The pair partner therefore lives in the same
+// wave64-native layout: ONE wavefront per (head, token), 4 per workgroup,
+// lane j holding the RoPE pair (x[j], x[j+64]). The pair partner therefore lives in the same
 // lane (no LDS round trip), the 128-element sum of squares is a 6-step xor
 // butterfly, and each 32-element Q8_0 block is one 32-lane half of the wave
 // (blocks 0/2 in lanes 0-31, blocks 1/3 in lanes 32-63).
@@ -19,12 +19,15 @@
 namespace bp {
 namespace {
 
-__global__ __launch_bounds__(64) void q_norm_rope_kernel(QNormRopeArgs a) {
-    const int j = threadIdx.x;
-    const uint32_t head = blockIdx.x, tok = blockIdx.y;
+// 4 waves per workgroup: wave w takes item 4 blockIdx.x + w of the
+// m_tokens x n_head (token-major) grid.
+__global__ __launch_bounds__(256) void q_norm_rope_kernel(QNormRopeArgs a) {
+    const int j = threadIdx.x & 63;
+    const uint32_t it = 4 * blockIdx.x + (threadIdx.x >> 6);
+    if (it >= a.n_items) return;
+    const uint32_t head = it % a.n_head, tok = it / a.n_head;
     uint16_t* q = a.act + a.q_off + static_cast<uint64_t>(tok) * a.q_dim + head * kHeadDim;
-    const uint16_t* cs =
-        a.rope_cs + static_cast<uint64_t>(a.pos_base + tok) * kHeadDim + 2 * j;
+    const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos_base + tok) * kHeadDim + 2 * j;
     float o0, o1;
     norm_rope_pair(h2f(q[j]), h2f(q[j + 64]), h2f(a.w_norms[a.w_off + j]),
                    h2f(a.w_norms[a.w_off + j + 64]), h2f(cs[0]), h2f(cs[1]), a.eps, o0, o1);
@@ -32,9 +35,13 @@ __global__ __launch_bounds__(64) void q_norm_rope_kernel(QNormRopeArgs a) {
     q[j + 64] = f2h(o1);
 }
 
-__global__ __launch_bounds__(64) void kv_writeback_kernel(KvWritebackArgs a) {
-    const int j = threadIdx.x;
-    const uint32_t head = blockIdx.x, tok = blockIdx.y;
+// 4 waves per workgroup: wave w takes (token, KV head) pair 4 blockIdx.x + w
+// (token-major).
+__global__ __launch_bounds__(256) void kv_writeback_kernel(KvWritebackArgs a) {
+    const int j = threadIdx.x & 63;
+    const uint32_t pr = 4 * blockIdx.x + (threadIdx.x >> 6);
+    if (pr >= a.n_pairs) return;
+    const uint32_t head = pr % a.n_kv_head, tok = pr / a.n_kv_head;
     const uint64_t tok_off = static_cast<uint64_t>(tok) * a.kv_dim + head * kHeadDim;
     const uint16_t* k = a.act + a.k_cur_off + tok_off;
     const uint16_t* v = a.act + a.v_cur_off + tok_off;
@@ -54,13 +61,19 @@ __global__ __launch_bounds__(64) void kv_writeback_kernel(KvWritebackArgs a) {
 
 hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t m_tokens,
                               hipStream_t s) {
-    hipLaunchKernelGGL(q_norm_rope_kernel, dim3(n_head, m_tokens), dim3(64), 0, s, a);
+    QNormRopeArgs b = a;
+    b.n_head = n_head;
+    b.n_items = n_head * m_tokens;
+    hipLaunchKernelGGL(q_norm_rope_kernel, dim3((b.n_items + 3) / 4), dim3(256), 0, s, b);
     return hipGetLastError();
 }
 
 hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uint32_t m_tokens,
                                hipStream_t s) {
-    hipLaunchKernelGGL(kv_writeback_kernel, dim3(n_kv_head, m_tokens), dim3(64), 0, s, a);
+    KvWritebackArgs b = a;
+    b.n_kv_head = n_kv_head;
+    b.n_pairs = n_kv_head * m_tokens;
+    hipLaunchKernelGGL(kv_writeback_kernel, dim3((b.n_pairs + 3) / 4), dim3(256), 0, s, b);
     return hipGetLastError();
 }
 

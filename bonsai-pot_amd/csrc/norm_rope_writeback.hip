@@ -1,60 +1,183 @@
 // Q-side norm+RoPE and K/V writeback into the Q8_0 cache, for gfx950.
 //
 // Restates src/shaders/q_norm_rope_fused.wgsl and
-// src/shaders/kv_writeback_fused.wgsl (reference repository) with a
-// wave64-native layout: ONE wavefront per (head, token), 4 per workgroup,
-// lane j holding the RoPE pair (x[j], x[j+64]). The pair partner therefore lives in the same
-// lane (no LDS round trip), the 128-element sum of squares is a 6-step xor
-// butterfly, and each 32-element Q8_0 block is one 32-lane half of the wave
-// (blocks 0/2 in lanes 0-31, blocks 1/3 in lanes 32-63).
+// src/shaders/kv_writeback_fused.wgsl (reference repository). Layout: 8 lanes
+// per (token, head) item, 8 items per wavefront (see kItemLanes below); the
+// fused decode step keeps the one-wave-per-item form of bp_norm_rope.hpp.
 //
 // Bit-exactness. Every f32 operation is one IEEE-rounded op in the order of
 // the reference shader (no contraction, correctly rounded sqrt and divide),
-// and the RMSNorm reduction uses the fixed butterfly order
-//   s_j = x_j*x_j + x_{j+64}*x_{j+64};  s += shfl_xor(s, 32, 16, 8, 4, 2, 1)
-// so cache bytes and f16 outputs match the CPU oracle bit for bit.
+// and the RMSNorm reduction uses the fixed pairing tree
+//   s_j = x_j*x_j + x_{j+64}*x_{j+64};  s += partner j ^ 32, 16, 8, 4, 2, 1
+// (the 64-lane xor butterfly of bp_norm_rope.hpp), so cache bytes and f16
+// outputs match the CPU oracle, and the fused decode path, bit for bit.
 #include "bp_kernels.hpp"
 #include "bp_norm_rope.hpp"
 
 namespace bp {
 namespace {
 
-// 4 waves per workgroup: wave w takes item 4 blockIdx.x + w of the
-// m_tokens x n_head (token-major) grid.
-__global__ __launch_bounds__(256) void q_norm_rope_kernel(QNormRopeArgs a) {
-    const int j = threadIdx.x & 63;
-    const uint32_t it = 4 * blockIdx.x + (threadIdx.x >> 6);
-    if (it >= a.n_items) return;
-    const uint32_t head = it % a.n_head, tok = it / a.n_head;
-    uint16_t* q = a.act + a.q_off + static_cast<uint64_t>(tok) * a.q_dim + head * kHeadDim;
-    const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos_base + tok) * kHeadDim + 2 * j;
-    float o0, o1;
-    norm_rope_pair(h2f(q[j]), h2f(q[j + 64]), h2f(a.w_norms[a.w_off + j]),
-                   h2f(a.w_norms[a.w_off + j + 64]), h2f(cs[0]), h2f(cs[1]), a.eps, o0, o1);
-    q[j] = f2h(o0);          // q_norm_rope_fused.wgsl:95
-    q[j + 64] = f2h(o1);
+// Standalone kernels: 8 lanes per (token, head) item, 8 items per wave, 4 waves
+// per workgroup. Lane L of an item holds dims 8L .. 8L+7 and their RoPE
+// partners 64 + 8L .. 64 + 8L+7, so loads and stores are 16-byte vectors and
+// the per-item scalar work (sqrt, the Q8_0 divides) is shared by 8 lanes
+// instead of 64. The RMSNorm sum reproduces the pairing tree of the 64-lane
+// butterfly exactly: partner j ^ 32 / 16 / 8 is lane L ^ 4 / 2 / 1 at the same
+// slot i, partner j ^ 4 / 2 / 1 is slot i ^ 4 / 2 / 1 of the same lane. Each
+// Q8_0 block is 4 lanes (block L / 4 for dims 8L.., 2 + L / 4 for 64 + 8L..).
+constexpr int kItemLanes = 8;
+
+template <bool kVec>
+__device__ __forceinline__ void load8(const uint16_t* p, float* out) {
+    if constexpr (kVec) {
+        const uint4 w = *reinterpret_cast<const uint4*>(p);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            out[2 * i] = h2f(static_cast<uint16_t>(u[i]));
+            out[2 * i + 1] = h2f(static_cast<uint16_t>(u[i] >> 16));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) out[i] = h2f(p[i]);
+    }
 }
 
-// 4 waves per workgroup: wave w takes (token, KV head) pair 4 blockIdx.x + w
-// (token-major).
+template <bool kVec>
+__device__ __forceinline__ void store8(uint16_t* p, const float* v) {
+    if constexpr (kVec) {
+        uint32_t u[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) u[i] = static_cast<uint32_t>(f2h(v[2 * i])) | (static_cast<uint32_t>(f2h(v[2 * i + 1])) << 16);
+        *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) p[i] = f2h(v[i]);
+    }
+}
+
+// RMSNorm * w + NEOX RoPE of one item in the 8-lane layout (same operations
+// as norm_rope_pair, per slot i): x0 = dims 8L + i, x1 = dims 64 + 8L + i.
+template <bool kVec>
+__device__ __forceinline__ void norm_rope8(float* x0, float* x1, const uint16_t* w, const uint16_t* cs_row,
+                                           int L, float eps) {
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) s[i] = x0[i] * x0[i] + x1[i] * x1[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) s[i] = s[i] + lane_xor<4>(s[i]);   // j ^ 32
+#pragma unroll
+    for (int i = 0; i < 8; i++) s[i] = s[i] + lane_xor<2>(s[i]);   // j ^ 16
+#pragma unroll
+    for (int i = 0; i < 8; i++) s[i] = s[i] + lane_xor<1>(s[i]);   // j ^ 8
+    const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];   // j ^ 4
+    const float sq = (t0 + t2) + (t1 + t3);                                                 // j ^ 2, j ^ 1
+    const float inv_h = 1.0f / sqrtf(sq / 128.0f + eps);
+    float w0[8], w1[8];
+    load8<kVec>(w + 8 * L, w0);
+    load8<kVec>(w + 64 + 8 * L, w1);
+    // cos/sin of pairs 8L .. 8L+7: 16 consecutive f16 of the table row.
+    const uint4 c0 = *reinterpret_cast<const uint4*>(cs_row + 16 * L);
+    const uint4 c1 = *reinterpret_cast<const uint4*>(cs_row + 16 * L + 8);
+    const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float c = h2f(static_cast<uint16_t>(cw[i])), sn = h2f(static_cast<uint16_t>(cw[i] >> 16));
+        const float n0 = x0[i] * inv_h * w0[i];
+        const float n1 = x1[i] * inv_h * w1[i];
+        x0[i] = n0 * c - n1 * sn;   // kv_writeback_fused.wgsl:102
+        x1[i] = n0 * sn + n1 * c;   // kv_writeback_fused.wgsl:107
+    }
+}
+
+// Q8_0 of the 8 values of one lane and its block (kv_writeback_fused.wgsl:118-200).
+__device__ __forceinline__ float quantize8(const float* x, uint2& packed) {
+    float a = fabsf(x[0]);
+#pragma unroll
+    for (int i = 1; i < 8; i++) a = fmaxf(a, fabsf(x[i]));
+    a = fmaxf(a, lane_xor<1>(a));
+    a = fmaxf(a, lane_xor<2>(a));
+    const float d = a / 127.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        b[i] = static_cast<uint32_t>(static_cast<int>(fminf(fmaxf(rintf(x[i] * inv), -127.0f), 127.0f))) & 0xffu;
+    packed.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    packed.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    return d;
+}
+
+__device__ __forceinline__ void quantize_store8(const float* x0, const float* x1, int L, float* d_row, int8_t* qs_row) {
+    uint2 p0, p1;
+    const float d0 = quantize8(x0, p0), d1 = quantize8(x1, p1);
+    *reinterpret_cast<uint2*>(qs_row + 8 * L) = p0;
+    *reinterpret_cast<uint2*>(qs_row + 64 + 8 * L) = p1;
+    if ((L & 3) == 0) {
+        d_row[L >> 2] = d0;        // elements [32 (L / 4), +32)
+        d_row[2 + (L >> 2)] = d1;  // elements [64 + 32 (L / 4), +32)
+    }
+}
+
+// Item it = 8 (4 blockIdx.x + wave) + lane / 8 of the m_tokens x n_head
+// (token-major) grid. Items past the end compute on a clamped item and store
+// nothing (the lane exchanges need every lane of the 8-lane group).
+template <bool kVec>
+__global__ __launch_bounds__(256) void q_norm_rope_kernel(QNormRopeArgs a) {
+    const int lane = threadIdx.x & 63, L = lane & (kItemLanes - 1);
+    const uint32_t it_raw = kItemLanes * (4 * blockIdx.x + (threadIdx.x >> 6)) + (lane >> 3);
+    const bool live = it_raw < a.n_items;
+    const uint32_t it = live ? it_raw : a.n_items - 1;
+    const uint32_t head = it % a.n_head, tok = it / a.n_head;
+    uint16_t* q = a.act + a.q_off + static_cast<uint64_t>(tok) * a.q_dim + head * kHeadDim;
+    float x0[8], x1[8];
+    load8<kVec>(q + 8 * L, x0);
+    load8<kVec>(q + 64 + 8 * L, x1);
+    norm_rope8<kVec>(x0, x1, a.w_norms + a.w_off, a.rope_cs + static_cast<uint64_t>(a.pos_base + tok) * kHeadDim, L,
+                     a.eps);
+    if (live) {
+        store8<kVec>(q + 8 * L, x0);   // q_norm_rope_fused.wgsl:95
+        store8<kVec>(q + 64 + 8 * L, x1);
+    }
+}
+
+// Item = (token, KV head) pair, same numbering as above: K gets norm + RoPE +
+// Q8_0, V Q8_0 only.
+template <bool kVec>
 __global__ __launch_bounds__(256) void kv_writeback_kernel(KvWritebackArgs a) {
-    const int j = threadIdx.x & 63;
-    const uint32_t pr = 4 * blockIdx.x + (threadIdx.x >> 6);
-    if (pr >= a.n_pairs) return;
+    const int lane = threadIdx.x & 63, L = lane & (kItemLanes - 1);
+    const uint32_t pr_raw = kItemLanes * (4 * blockIdx.x + (threadIdx.x >> 6)) + (lane >> 3);
+    const bool live = pr_raw < a.n_pairs;
+    const uint32_t pr = live ? pr_raw : a.n_pairs - 1;
     const uint32_t head = pr % a.n_kv_head, tok = pr / a.n_kv_head;
     const uint64_t tok_off = static_cast<uint64_t>(tok) * a.kv_dim + head * kHeadDim;
     const uint16_t* k = a.act + a.k_cur_off + tok_off;
     const uint16_t* v = a.act + a.v_cur_off + tok_off;
     const uint64_t row = static_cast<uint64_t>(a.pos_base) + tok;
-    const uint16_t* cs = a.rope_cs + row * kHeadDim + 2 * j;
-    float k0, k1;
-    norm_rope_pair(h2f(k[j]), h2f(k[j + 64]), h2f(a.w_norms[a.w_off + j]),
-                   h2f(a.w_norms[a.w_off + j + 64]), h2f(cs[0]), h2f(cs[1]), a.eps, k0, k1);
+    float k0[8], k1[8], v0[8], v1[8];
+    load8<kVec>(k + 8 * L, k0);
+    load8<kVec>(k + 64 + 8 * L, k1);
+    load8<kVec>(v + 8 * L, v0);
+    load8<kVec>(v + 64 + 8 * L, v1);
+    norm_rope8<kVec>(k0, k1, a.w_norms + a.w_off, a.rope_cs + row * kHeadDim, L, a.eps);
     const uint64_t nb_row = a.kv_dim / kBlock;
     const uint64_t d_idx = row * nb_row + head * (kHeadDim / kBlock);
     const uint64_t qs_idx = row * a.kv_dim + head * kHeadDim;
-    quantize_store_pair(k0, k1, j, a.k_d + d_idx, a.k_qs + qs_idx);
-    quantize_store_pair(h2f(v[j]), h2f(v[j + 64]), j, a.v_d + d_idx, a.v_qs + qs_idx);
+    uint2 pk0, pk1, pv0, pv1;
+    const float dk0 = quantize8(k0, pk0), dk1 = quantize8(k1, pk1);
+    const float dv0 = quantize8(v0, pv0), dv1 = quantize8(v1, pv1);
+    if (live) {
+        *reinterpret_cast<uint2*>(a.k_qs + qs_idx + 8 * L) = pk0;
+        *reinterpret_cast<uint2*>(a.k_qs + qs_idx + 64 + 8 * L) = pk1;
+        *reinterpret_cast<uint2*>(a.v_qs + qs_idx + 8 * L) = pv0;
+        *reinterpret_cast<uint2*>(a.v_qs + qs_idx + 64 + 8 * L) = pv1;
+        if ((L & 3) == 0) {
+            a.k_d[d_idx + (L >> 2)] = dk0;
+            a.k_d[d_idx + 2 + (L >> 2)] = dk1;
+            a.v_d[d_idx + (L >> 2)] = dv0;
+            a.v_d[d_idx + 2 + (L >> 2)] = dv1;
+        }
+    }
 }
 
 }  // namespace
@@ -64,7 +187,13 @@ hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t 
     QNormRopeArgs b = a;
     b.n_head = n_head;
     b.n_items = n_head * m_tokens;
-    hipLaunchKernelGGL(q_norm_rope_kernel, dim3((b.n_items + 3) / 4), dim3(256), 0, s, b);
+    const dim3 grid((b.n_items + 4 * kItemLanes - 1) / (4 * kItemLanes));
+    // 16-byte vectors when the caller's offsets allow them.
+    if ((b.q_off | b.w_off | b.q_dim) % 8 == 0 && reinterpret_cast<uintptr_t>(b.act) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(b.w_norms) % 16 == 0)
+        hipLaunchKernelGGL(q_norm_rope_kernel<true>, grid, dim3(256), 0, s, b);
+    else
+        hipLaunchKernelGGL(q_norm_rope_kernel<false>, grid, dim3(256), 0, s, b);
     return hipGetLastError();
 }
 
@@ -73,7 +202,12 @@ hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uin
     KvWritebackArgs b = a;
     b.n_kv_head = n_kv_head;
     b.n_pairs = n_kv_head * m_tokens;
-    hipLaunchKernelGGL(kv_writeback_kernel, dim3((b.n_pairs + 3) / 4), dim3(256), 0, s, b);
+    const dim3 grid((b.n_pairs + 4 * kItemLanes - 1) / (4 * kItemLanes));
+    if ((b.k_cur_off | b.v_cur_off | b.w_off) % 8 == 0 && reinterpret_cast<uintptr_t>(b.act) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(b.w_norms) % 16 == 0)
+        hipLaunchKernelGGL(kv_writeback_kernel<true>, grid, dim3(256), 0, s, b);
+    else
+        hipLaunchKernelGGL(kv_writeback_kernel<false>, grid, dim3(256), 0, s, b);
     return hipGetLastError();
 }
 

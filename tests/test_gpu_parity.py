@@ -48,6 +48,26 @@ def test_writeback_and_q_norm_rope_bit_exact(cuda, m, pos_base, w_std):
     assert np.array_equal(act, sc.act), "q_norm_rope f16 output differs"
 
 
+@pytest.mark.parametrize("m", [1, 9, 64])
+def test_writeback_and_q_norm_rope_unaligned_offsets(cuda, m):
+    """Element offsets that are not multiples of 8 (the kernels then use 2-byte
+    loads and stores instead of 16-byte vectors): same bits as the oracle."""
+    _say(f"[writeback] unaligned offsets m={m}")
+    cfg = layout.Config(n_layer=2)
+    sc = Scenario(cfg, max_seq=256, m_tokens=m, seed=100 + m, w_std=0.1)
+    sc.q_off, sc.k_off, sc.v_off = 3, sc.k_off + 5, sc.v_off + 7
+    sc.w_q_off, sc.w_k_off = 1, 127
+    dev = DeviceScenario(sc)
+    dev.writeback(il=1, pos_base=40)
+    dev.q_norm_rope(40)
+    sc.oracle_writeback(il=1, pos_base=40)
+    sc.oracle_q_norm_rope(40)
+    k, v = dev.kv_host()
+    assert np.array_equal(k, sc.kv_k), f"K cache bytes differ at {np.flatnonzero(k != sc.kv_k)[:8]}"
+    assert np.array_equal(v, sc.kv_v), f"V cache bytes differ at {np.flatnonzero(v != sc.kv_v)[:8]}"
+    assert np.array_equal(dev.act_host(), sc.act), "q_norm_rope f16 output differs"
+
+
 def test_writeback_special_values(cuda):
     """All-zero heads (d = 0 path), tiny subnormal f16 V values, +-max f16."""
     _say("[writeback] special values")

@@ -108,7 +108,10 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
     const int t = threadIdx.x;
-    const uint32_t c = blockIdx.x, g = blockIdx.y;
+    // 1-D grid, KV head fastest (as in prefill_kernel): head g's chunks are
+    // written on the XCD whose L2 serves head g in the attention pass.
+    const uint32_t nkv = a.kv_dim / kHeadDim;
+    const uint32_t g = blockIdx.x % nkv, c = blockIdx.x / nkv;
     const uint32_t nb_row = a.kv_dim / kBlock;
     const uint32_t last = a.n_rows - 1;
     // ---- loads (unconditional, clamped rows; rows past n_rows get d = 0) ----
@@ -450,7 +453,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(kv_dequant_kernel, dim3((a.n_rows + kChunk - 1) / kChunk, n_kv_head), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(kv_dequant_kernel, dim3((a.n_rows + kChunk - 1) / kChunk * n_kv_head), dim3(256), 0, s, a);
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
     hipLaunchKernelGGL(prefill_kernel, dim3(n_pairs * n_kv_head), dim3(kThreads), 0, s, a);
     return hipGetLastError();

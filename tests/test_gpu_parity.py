@@ -31,11 +31,11 @@ def _prefill_cache(sc: Scenario, il: int, n_rows: int, seed: int):
 
 
 @pytest.mark.parametrize("m,pos_base,w_std", [(1, 0, 0.0), (1, 512, 0.1), (7, 33, 0.1),
-                                              (512, 0, 0.0), (300, 1700, 0.1)])
+                                              (512, 0, 0.0), (300, 1700, 0.1), (2048, 2048, 0.1)])
 def test_writeback_and_q_norm_rope_bit_exact(cuda, m, pos_base, w_std):
     _say(f"[writeback] m={m} pos_base={pos_base} w_std={w_std}")
     cfg = layout.Config(n_layer=3)
-    sc = Scenario(cfg, max_seq=2048, m_tokens=m, seed=m + pos_base, w_std=w_std)
+    sc = Scenario(cfg, max_seq=4096, m_tokens=m, seed=m + pos_base, w_std=w_std)
     dev = DeviceScenario(sc)
     dev.writeback(il=2, pos_base=pos_base)
     dev.q_norm_rope(pos_base)

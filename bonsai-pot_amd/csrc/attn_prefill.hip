@@ -14,7 +14,9 @@
 //    wave's MFMA columns). A 512-thread workgroup owns one KV head and a
 //    zig-zag PAIR of tiles: light tile A = p, heavy tile B = n_tiles-1-p
 //    (1-D grid, KV head fastest: one head per XCD). Wave w (SIMD w & 3) owns
-//    unit (w & 3) of tile A if w < 4, of tile B otherwise.
+//    unit (w & 3) of tile A if w < 4, of tile B otherwise. For short prompts
+//    (fewer tile pairs x KV heads than CUs) a unit is 16 tokens x 1 head and
+//    two workgroups split the 4 query heads of a (KV head, pair).
 //  * Work balance (split-K inside the workgroup): with n_A / n_B the 64-row
 //    chunks tiles A / B attend and mid = ceil((n_A + n_B) / 2), the B waves
 //    take B's chunks [0, mid) while the A waves take A's chunks [0, n_A) and
@@ -50,7 +52,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 512;
-constexpr int kHeadsPerWave = 2;
 constexpr int kChunk = 64;               // cache rows per LDS chunk
 constexpr int kSub = kChunk / 16;        // 16-row S^T sub-tiles per chunk
 constexpr int kKHalves = kChunk * kHeadDim;   // K rows, 256 B each
@@ -182,7 +183,14 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
         *reinterpret_cast<U4*>(vdst + v_addr(dim, (s0 >> 3) + i)) = *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
 }
 
+// kHpw query heads per wave: 2 (a workgroup covers all 4 heads of its KV
+// head), or 1 for short prompts, where two workgroups (head sets) share a
+// (KV head, tile pair) and every wave does half the work, so that twice the
+// workgroups run.
+template <int kHpw>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+    constexpr int kHeadsPerWave = kHpw;
+    constexpr int kHeadSets = 2 / kHpw;
     // lds[stream][buf]: staged chunk (K rows then V^T rows), 2 streams x 2 buffers.
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
 
@@ -194,9 +202,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // so with 8 KV heads each XCD serves one head and its L2 holds that head's
     // K/V for all the head's tile pairs.
     const uint32_t nkv = a.kv_dim / kHeadDim;
-    const uint32_t g = blockIdx.x % nkv, pair = blockIdx.x / nkv;
+    const uint32_t g = blockIdx.x % nkv, rest = blockIdx.x / nkv;
+    const uint32_t hs = rest % kHeadSets, pair = rest / kHeadSets;
     const uint32_t tile_a = pair, tile_b = a.n_tiles - 1 - pair;   // tile_b >= tile_a
-    const uint32_t h0 = g * kGroup + kHeadsPerWave * ((wave >> 1) & 1);        // first query head
+    const uint32_t h0 = g * kGroup + 2 * hs + kHeadsPerWave * ((wave >> 1) & 1);   // first query head
     const uint32_t utok = 16 * (wave & 1);            // unit's first token within its tile
     const float c2 = a.scale * 1.4426950408889634f;   // scores in log2 units
 
@@ -337,7 +346,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             // which f16 P and the f32 accumulators hold as well as p <= 1.
             up[h] = cm[h] > m_run[h] + kLazy;
         }
-        if (__any(up[0] || up[1])) {
+        bool any_up = false;
+#pragma unroll
+        for (int h = 0; h < kHeadsPerWave; h++) any_up = any_up || up[h];
+        if (__any(any_up)) {
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++) {
                 const float m_new = up[h] ? cm[h] : m_run[h];
@@ -455,7 +467,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
     hipLaunchKernelGGL(kv_dequant_kernel, dim3((a.n_rows + kChunk - 1) / kChunk * n_kv_head), dim3(256), 0, s, a);
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
-    hipLaunchKernelGGL(prefill_kernel, dim3(n_pairs * n_kv_head), dim3(kThreads), 0, s, a);
+    if (a.heads_per_wave == 1)
+        hipLaunchKernelGGL(prefill_kernel<1>, dim3(2 * n_pairs * n_kv_head), dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL(prefill_kernel<2>, dim3(n_pairs * n_kv_head), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
-// Per-head RMSNorm * weight + NEOX RoPE and the Q8_0 quantizer, shared by the
-// standalone q_norm_rope / kv_writeback kernels and the fused decode step so
-// that every path produces the same bits.
+// Per-head RMSNorm * weight + NEOX RoPE and the Q8_0 quantizer in the
+// one-wave-per-head form used by the fused decode step. The standalone
+// q_norm_rope / kv_writeback kernels (norm_rope_writeback.hip) run 8 lanes per
+// head with the same pairing tree, so every path produces the same bits.
 //
 // Layout: one 64-lane wavefront per 128-wide head, lane j holding the RoPE
 // pair (x[j], x[j+64]); the lane exchanges of strides 1-8 are DPP moves. Every f32 operation is one IEEE-rounded op in the

@@ -335,16 +335,26 @@ def bench_matvec(torch, args, n_layer=36):
                    "GBps": byt / (us * 1e-6) / 1e9, "frac_hbm": byt / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
     b.model.close()
     res["lm_head"] = bench_lm_head(torch, args)
+    res["lm_head_mfma_opt_in"] = bench_lm_head(torch, args, arith="mfma")
     return res
 
 
-def bench_lm_head(torch, args, vocab=151936, n_copies=8):
+def bench_lm_head(torch, args, vocab=151936, n_copies=8, arith=None):
     """The LM head matvec (vocab x 2560 Q1_0, 54.7 MB) over 8 copies of the
-    weights (438 MB, above the Infinity Cache)."""
+    weights (438 MB, above the Infinity Cache). arith None: the default
+    arithmetic (the reference's f16 sums); "mfma": the opt-in i8-MFMA kernel."""
     from bonsai_pot_amd import Model, layout
     H = MatvecLayers.HIDDEN
     nb = H // 128
-    m = Model(layout.Config(n_layer=1), 64)
+    old = os.environ.pop("BP_MATVEC_ARITH", None)
+    if arith is not None:
+        os.environ["BP_MATVEC_ARITH"] = arith
+    try:
+        m = Model(layout.Config(n_layer=1), 64)
+    finally:
+        os.environ.pop("BP_MATVEC_ARITH", None)
+        if old is not None:
+            os.environ["BP_MATVEC_ARITH"] = old
     m.set_stream(torch.cuda.current_stream().cuda_stream)
     g = torch.Generator(device="cuda").manual_seed(7)
     d_bytes = 2 * vocab * nb
@@ -438,10 +448,39 @@ def measured_traffic(workload, kernel):
     return hits[0] if len(hits) == 1 else None
 
 
+def _cpu_info():
+    """CPU model name and the machine's physical core count (from /proc/cpuinfo)."""
+    name, cores = "unknown", set()
+    try:
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and name == "unknown":
+                    name = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    return name, len(cores) or None
+
+
 def cpu_baseline(seconds=10.0):
-    """CPU oracle (scalar C restatement of the reference's split/merge decode),
-    1 thread, decode at ctx 4096 over as many layers as fit in ~seconds."""
+    """CPU oracle (plain-C restatement of the reference's split/merge decode)
+    on the host: decode at ctx 4096, one layer-decode per call, run by a pool
+    of threads (the C calls release the GIL), each on its own output buffer,
+    for ~seconds. Threads = this process's CPU share, capped at 16 (the GPU
+    box grants 16 host CPUs to a one-GPU job)."""
     import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     from bonsai_pot_amd import layout
@@ -454,24 +493,41 @@ def cpu_baseline(seconds=10.0):
         nd = n_layer * max_seq * 32
         buf[:nd * 4].view(np.float32)[:] = np.float32(0.02)
         kv.append(buf)
-    act = rng.standard_normal(2 * 4096).astype(np.float16).view(np.uint16)
-    layers = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        il = layers % n_layer
+    act0 = rng.standard_normal(2 * 4096).astype(np.float16).view(np.uint16)
+    try:
+        share = len(os.sched_getaffinity(0))
+    except AttributeError:
+        share = os.cpu_count() or 1
+    threads = max(1, min(share, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16))
+    params = []
+    for il in range(n_layer):
         d_word, qs_byte = layout.kv_layer_offsets(n_layer, 1024, max_seq, il)
-        p = orc.AttnSplitParams(head_dim=128, n_head=32, n_kv_head=8, pos=n_keys, kv_stride=1024,
-                                q_offset=0, k_d_word_offset=d_word, k_qs_byte_offset=qs_byte,
-                                v_d_word_offset=d_word, v_qs_byte_offset=qs_byte,
-                                n_chunks_active=(n_keys + 15) // 16, scale=128 ** -0.5,
-                                out_offset=4096)
-        orc.attention_split_merge(p, act, kv[0], kv[1])
-        layers += 1
+        params.append(orc.AttnSplitParams(head_dim=128, n_head=32, n_kv_head=8, pos=n_keys, kv_stride=1024,
+                                          q_offset=0, k_d_word_offset=d_word, k_qs_byte_offset=qs_byte,
+                                          v_d_word_offset=d_word, v_qs_byte_offset=qs_byte,
+                                          n_chunks_active=(n_keys + 15) // 16, scale=128 ** -0.5,
+                                          out_offset=4096))
+    t_end = [0.0]
+
+    def worker(tid):
+        act = act0.copy()
+        done = 0
+        while time.perf_counter() < t_end[0]:
+            orc.attention_split_merge(params[(tid + done) % n_layer], act, kv[0], kv[1])
+            done += 1
+        return done
+
+    t0 = time.perf_counter()
+    t_end[0] = t0 + seconds
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        layers = sum(ex.map(worker, range(threads)))
     dt = time.perf_counter() - t0
-    return {"value": decode_bytes(n_keys) * layers / dt / 1e9, "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"{layers} layer-decodes at ctx 4096 (4097 rows, 32 q heads) in {dt:.1f} s, "
-                      "scalar C oracle restating attention_split + attention_merge"}
+    name, phys = _cpu_info()
+    return {"value": decode_bytes(n_keys) * layers / dt / 1e9, "unit": "GB/s", "cores": threads,
+            "kind": "port", "cpu": name, "cpu_physical_cores_on_host": phys, "cpu_share": share,
+            "sample": f"{layers} layer-decodes at ctx 4096 (4097 rows, 32 q heads) in {dt:.1f} s on "
+                      f"{threads} threads, plain-C oracle restating attention_split + attention_merge "
+                      "(the reference's WGSL on lavapipe cannot run here: no Vulkan loader/ICD, no Rust)"}
 
 
 def roofline_decode(d4):

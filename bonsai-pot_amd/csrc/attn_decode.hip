@@ -128,6 +128,10 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     if (split >= a.n_splits) return;
     const uint32_t row0 = min(split * a.split_len, a.n_rows);
     const uint32_t row_end = min(row0 + a.split_len, a.n_rows);
+    // Last row a load may touch: row 0 when the range is empty (the fused step
+    // at pos 0 streams no rows but still issues its unconditional first batch;
+    // row 0 of the layer always exists since max_seq >= 1).
+    const uint32_t row_last = row_end > 0 ? row_end - 1 : 0u;
     const float c2 = a.scale * kLog2e;   // scores in log2 units
 
     const uint32_t kv_dim = a.kv_dim;
@@ -138,12 +142,12 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     const uint32_t dcol = g * (kHeadDim / kBlock) + bq;    // scale of block bq
     auto load = [&](Batch& B, uint32_t b) {
         const uint32_t r0 = row0 + 16u * (kRowSets * b + rs);
-        const uint32_t rk = min(r0 + lr, row_end - 1);
+        const uint32_t rk = min(r0 + lr, row_last);
         B.kq[0] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol));
         B.kq[1] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol + 16));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t rr = min(r0 + 4u * lg + j, row_end - 1);
+            const uint32_t rr = min(r0 + 4u * lg + j, row_last);
             B.kd[j] = a.k.d[rr * nb_row + dcol];
             B.vd[j] = a.v.d[rr * nb_row + dcol];
             B.vv[j] = *reinterpret_cast<const u32x2*>(a.v.qs + (rr * kv_dim + vcol));

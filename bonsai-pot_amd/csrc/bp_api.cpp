@@ -21,6 +21,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -43,7 +44,7 @@ struct bp_model {
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
     uint32_t prefill_hpw;   // 0 = by grid size, else 1 or 2 query heads per prefill wave
-    int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 f16 sums in the reference's order, 2 i8 MFMA
+    int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 (default) f16 sums in the reference's order, 2 i8 MFMA
     uint32_t matvec_stream_min_tiles;
     bool lost;
     std::string lost_message;
@@ -214,6 +215,14 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
                     cfg->n_kv_head);
     if (cfg->n_layer == 0) return fail(BP_ERR_CONFIG, "n_layer must be > 0");
     if (max_seq == 0) return fail(BP_ERR_CONFIG, "max_seq must be > 0");
+    // The kernels address a row inside one layer's section with 32-bit
+    // offsets (row * kv_dim + column): one layer's qs section must stay below
+    // 4 GiB. The reference keeps whole-buffer offsets in u32
+    // (src/forward.rs:48-58) and rejects caches above the adapter's buffer
+    // limit with PotError::Config (src/model.rs:1189-1198).
+    if (static_cast<uint64_t>(max_seq) * cfg->n_kv_head * cfg->head_dim > 0xFFFFFFFFull)
+        return fail(BP_ERR_CONFIG, "max_seq %u x kv_dim %u exceeds the 32-bit per-layer cache offsets; reduce max_seq",
+                    max_seq, cfg->n_kv_head * cfg->head_dim);
     if (!(cfg->rms_eps >= 0.0f) || !(cfg->rope_freq_base > 0.0f))
         return fail(BP_ERR_CONFIG, "rms_eps must be >= 0 and rope_freq_base > 0");
     int n_dev = 0;
@@ -241,13 +250,13 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
 
     m->kv_bytes = bp_kv_buffer_bytes(cfg->n_layer, m->kv_dim, max_seq);
     // Split-K partials: n_head x (at most decode_max_splits()) x stride floats.
-    m->decode_min_split_rows = 128;
+    m->decode_min_split_rows = bp::kDecodeMinSplitRows;
     if (const char* env = std::getenv("BP_DECODE_MIN_SPLIT_ROWS")) {
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 32 && v <= (1 << 20)) m->decode_min_split_rows = static_cast<uint32_t>(v);
     }
     // Rows from which the split pass reads 4 KV heads per workgroup.
-    m->decode_wide_min_rows = 8192;
+    m->decode_wide_min_rows = bp::kDecodeWideMinRows;
     if (const char* env = std::getenv("BP_DECODE_WIDE_MIN_ROWS")) {
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 0) m->decode_wide_min_rows = static_cast<uint32_t>(v);
@@ -257,13 +266,15 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
         const long v = std::strtol(env, nullptr, 10);
         if (v == 1 || v == 2) m->prefill_hpw = static_cast<uint32_t>(v);
     }
-    // Q1_0 matvec arithmetic: "f16" = the reference's f16 sums, bit for bit
-    // (VALU-bound); "mfma" = exact integer sums of 15-bit x on the i8 matrix
-    // cores; default "auto" = f16 below the streaming size, MFMA from it on
-    // (the LM head), where the f16 kernel's VALU work exceeds its HBM time.
-    m->matvec_arith = 0;
+    // Q1_0 matvec arithmetic. Default "f16": the reference's f16 block sums in
+    // its order, bit for bit (VALU-bound), so logits and hence top-k token
+    // choices equal the reference's. Opt-in "mfma": exact integer sums of x
+    // rounded to 15 bits per block on the i8 matrix cores (closer to the
+    // exact product, not the reference's bits); "auto": f16 below the
+    // streaming size, MFMA from it on (the LM head, 2.2x faster there).
+    m->matvec_arith = 1;
     if (const char* env = std::getenv("BP_MATVEC_ARITH")) {
-        if (std::strcmp(env, "f16") == 0) m->matvec_arith = 1;
+        if (std::strcmp(env, "auto") == 0) m->matvec_arith = 0;
         else if (std::strcmp(env, "mfma") == 0) m->matvec_arith = 2;
     }
     // MFMA matvec: 16-row tiles from which each wave streams whole tiles.
@@ -311,8 +322,14 @@ void bp_model_destroy(bp_model* m) {
 }
 
 bp_status bp_model_set_stream(bp_model* m, void* stream) {
-    bp_status st = check_model(m);
+    bp_status st = enter(m);
     if (st != BP_OK) return st;
+    // The model's scratch (split-K partials, normalized q, the prefill f16
+    // image) is shared by every launch: work still queued on the old stream
+    // must finish before the new stream may reuse it.
+    if (m->stream != static_cast<hipStream_t>(stream) &&
+        (st = hip_check(m, hipStreamSynchronize(m->stream), "set_stream: drain old stream")) != BP_OK)
+        return st;
     m->stream = static_cast<hipStream_t>(stream);
     return BP_OK;
 }
@@ -707,6 +724,90 @@ static bp_status snapshot_copy(bp_model* m, uint32_t pos, uint8_t* payload, uint
         }
     }
     return hip_check(m, hipStreamSynchronize(m->stream), "snapshot sync");
+}
+
+// ---- allocation-free decode ---------------------------------------------------
+// Split-K partials for bp_attention_decode_noalloc live in this file-scope
+// device array instead of memory the library allocates: 64 query heads x 128
+// splits (the most decode_plan makes) x 132 floats per partial = 4.125 MiB, so
+// every context fits at n_head <= 64. Every GPU holds its own copy until the
+// process ends.
+// In host code `scratch` is only a stand-in for the symbol: kernels get the
+// device address from hipGetSymbolAddress, looked up once per device.
+constexpr uint64_t kNoAllocScratchFloats = 64ull * 128 * 132;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+constexpr int kNoAllocMaxDevices = 64;
+struct NoAllocDevice {
+    std::once_flag once;
+    hipError_t status = hipSuccess;
+    float* ptr = nullptr;   // device address of `scratch` on this device
+    int cu_count = 0;
+};
+static NoAllocDevice g_noalloc[kNoAllocMaxDevices];
+
+// Once per device, with that device current: the device address of this
+// device's `scratch` and its CU count (for the split plan).
+static NoAllocDevice* noalloc_setup(int dev) {
+    NoAllocDevice* d = &g_noalloc[dev];
+    std::call_once(d->once, [d, dev]() {
+        void* p = nullptr;
+        d->status = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (d->status == hipSuccess)
+            d->status = hipDeviceGetAttribute(&d->cu_count, hipDeviceAttributeMultiprocessorCount, dev);
+        d->ptr = static_cast<float*>(p);
+    });
+    return d;
+}
+
+bp_status bp_attention_decode_noalloc(const bp_config* cfg, void* kv_k, void* kv_v, uint32_t max_seq, void* act,
+                                      uint32_t q_off, uint32_t out_off, uint32_t layer_il, uint32_t pos,
+                                      void* stream) {
+    if (!cfg || !kv_k || !kv_v || !act) return fail(BP_ERR_INVALID_ARG, "cfg/kv_k/kv_v/act is NULL");
+    if (cfg->head_dim != bp::kHeadDim)
+        return fail(BP_ERR_CONFIG, "head_dim must be 128 (got %u)", cfg->head_dim);
+    if (cfg->n_kv_head == 0 || cfg->n_head != cfg->n_kv_head * bp::kGroup)
+        return fail(BP_ERR_CONFIG, "n_head must be 4 * n_kv_head (got %u, %u)", cfg->n_head, cfg->n_kv_head);
+    if (layer_il >= cfg->n_layer) return fail(BP_ERR_INVALID_ARG, "layer %u >= n_layer %u", layer_il, cfg->n_layer);
+    const uint32_t kv_dim = cfg->n_kv_head * cfg->head_dim;
+    if (static_cast<uint64_t>(max_seq) * kv_dim > 0xFFFFFFFFull)
+        return fail(BP_ERR_CONFIG, "max_seq %u x kv_dim %u exceeds the 32-bit per-layer cache offsets", max_seq, kv_dim);
+    if (pos >= max_seq)
+        return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens 1 > max_seq %u", pos, max_seq);
+    if ((q_off & 7u) || (out_off & 3u))
+        return fail(BP_ERR_INVALID_ARG, "q_off must be a multiple of 8 and out_off of 4 (aligned f16 rows)");
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(BP_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kNoAllocMaxDevices) return fail(BP_ERR_INVALID_ARG, "device %d out of range", dev);
+    NoAllocDevice* d = noalloc_setup(dev);
+    if (d->status != hipSuccess)
+        return fail(BP_ERR_HIP, "scratch symbol lookup on device %d: %s", dev, hipGetErrorString(d->status));
+
+    bp::DecodeArgs a{};
+    a.q = static_cast<const uint16_t*>(act) + q_off;
+    a.out = static_cast<uint16_t*>(act) + out_off;
+    const uint64_t nb = kv_dim / 32;
+    const uint64_t d_word = static_cast<uint64_t>(layer_il) * max_seq * nb;
+    const uint64_t qs_byte = static_cast<uint64_t>(cfg->n_layer) * max_seq * nb * 4 +
+                             static_cast<uint64_t>(layer_il) * max_seq * kv_dim;
+    a.k.d = static_cast<const float*>(kv_k) + d_word;
+    a.k.qs = static_cast<const int8_t*>(kv_k) + qs_byte;
+    a.v.d = static_cast<const float*>(kv_v) + d_word;
+    a.v.qs = static_cast<const int8_t*>(kv_v) + qs_byte;
+    a.partials = d->ptr;
+    a.kv_dim = kv_dim;
+    a.n_rows = pos + 1;   // src/forward.rs:822
+    bp::decode_plan(a.n_rows, cfg->n_kv_head, d->cu_count, bp::kDecodeMinSplitRows, bp::kDecodeWideMinRows,
+                    &a.split_len, &a.n_splits, &a.heads_per_wg);
+    a.scale = 1.0f / std::sqrt(static_cast<float>(cfg->head_dim));   // src/forward.rs:838
+    if (static_cast<uint64_t>(a.n_splits) * cfg->n_head * bp::decode_partial_stride() > kNoAllocScratchFloats)
+        return fail(BP_ERR_CONFIG, "noalloc decode: %u query heads x %u splits exceed the %llu-float scratch",
+                    cfg->n_head, a.n_splits, static_cast<unsigned long long>(kNoAllocScratchFloats));
+    bp::launch_decode(a, cfg->n_kv_head, static_cast<hipStream_t>(stream));
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(BP_ERR_HIP, "attention_decode_noalloc launch: %s", hipGetErrorString(e));
+    return BP_OK;
 }
 
 bp_status bp_kv_snapshot_capture(bp_model* m, uint32_t pos, void* payload, uint64_t payload_bytes) {

@@ -12,6 +12,10 @@ constexpr uint32_t kHeadDim = 128;   // Bonsai head_dim (src/model.rs:1179-1183)
 constexpr uint32_t kGroup = 4;       // Q heads per KV head (attention_split.wgsl:150)
 constexpr uint32_t kBlock = 32;      // Q8_0 block (src/forward.rs:40-47)
 constexpr uint32_t kPrefillTileTok = 32;   // query tokens per prefill tile
+// Default split-K plan of decode_plan: fewest rows per split, and the row
+// count from which the split pass reads 4 KV heads per workgroup.
+constexpr uint32_t kDecodeMinSplitRows = 128;
+constexpr uint32_t kDecodeWideMinRows = 8192;
 
 // One (layer, kind) view of a Q8_0 KV buffer: FP32 scales at d (index
 // (row*kv_dim + e)/32), int8 quants at qs (index row*kv_dim + e).

@@ -74,11 +74,14 @@ typedef struct bp_model bp_model;
 
 /* Creates the device-side state the attention path owns: kv_k, kv_v (zeroed),
  * the f16 RoPE table for positions [0, max_seq) and the split-K partials
- * scratch. `device` is a HIP device ordinal. */
+ * scratch. `device` is a HIP device ordinal. BP_ERR_CONFIG when
+ * max_seq * kv_dim exceeds 2^32 (the kernels' per-layer offsets are 32-bit). */
 bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp_model** out);
 void bp_model_destroy(bp_model* model);
 
-/* Stream all later calls are ordered on (a hipStream_t; NULL = the null stream). */
+/* Stream all later calls are ordered on (a hipStream_t; NULL = the null stream).
+ * Switching to another stream first waits for the old stream to drain, since
+ * the model's scratch buffers are shared by all launches. */
 bp_status bp_model_set_stream(bp_model* model, void* stream);
 /* Blocks until the model's stream is idle; latches device loss on failure. */
 bp_status bp_model_synchronize(bp_model* model);
@@ -220,6 +223,24 @@ bp_status bp_kv_snapshot_apply(bp_model* model, uint32_t pos, const void* payloa
  * touching the GPU). */
 bp_status bp_check_device(const bp_model* model);
 bp_status bp_debug_lose_device(bp_model* model);
+
+/* Allocation-free single-token decode. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same result
+ * and kernels as bp_dispatch_attention_decode — rows [0, pos] of layer
+ * `layer_il`, q already normalized at act[q_off], output at act[out_off] —
+ * but it needs no bp_model: the caller passes its own kv_k / kv_v buffers (the
+ * reference byte layout for cfg->n_layer x max_seq), and the split-K partials
+ * live in a fixed 4.125 MiB device array inside the library (one per GPU, kept
+ * until the process ends), so the call never allocates. Launches on `stream`
+ * on the current device. BP_ERR_CONFIG when n_head x the split count of
+ * pos + 1 rows does not fit that array (it fits every context at n_head <= 64).
+ * Calls that overlap on one GPU share the array and race: serialize them
+ * (one stream, or events between streams). Nothing in the array needs to
+ * start at zero: every partial is written before it is read. */
+bp_status bp_attention_decode_noalloc(const bp_config* cfg, void* kv_k, void* kv_v, uint32_t max_seq, void* act,
+                                      uint32_t q_off, uint32_t out_off, uint32_t layer_il, uint32_t pos,
+                                      void* stream);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* bp_last_error(void);

@@ -16,6 +16,9 @@ from bonsai_pot_amd.layout import Config, kv_buffer_bytes, kv_layer_offsets
 
 TOL_MAX_ABS = 2e-3      # attention output vs f32-softmax oracle
 TOL_REL_L2 = 1e-3
+# (what, max_abs, rel_l2) of every attention comparison in this process; the
+# session summary (tests/conftest.py) prints them with their margin to the bar.
+MARGINS = []
 
 
 class Scenario:
@@ -188,7 +191,31 @@ def assert_attn_close(got: np.ndarray, want: np.ndarray, what: str = "attention"
     err = np.abs(got - want)
     max_abs = float(err.max())
     rel_l2 = float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+    MARGINS.append((what, max_abs, rel_l2))
     assert max_abs <= TOL_MAX_ABS and rel_l2 <= TOL_REL_L2, (
         f"{what}: max_abs {max_abs:.3e} (<= {TOL_MAX_ABS}), rel_l2 {rel_l2:.3e} (<= {TOL_REL_L2}) "
         f"worst at {np.unravel_index(int(err.argmax()), err.shape)}")
     return max_abs, rel_l2
+
+
+def write_outlier_rows(sc: Scenario, il: int, n_rows: int, seed: int, frac: float = 0.01):
+    """Oracle-written cache rows [0, n_rows) of layer il from an independent
+    seeded K/V scenario, with `frac` of the rows' K scaled x8 before
+    quantization (a w_k_norm of 8.0 for those rows, exact in f16) — the
+    softmax max-tracking stress of BASELINE configs[4]. Returns the rows."""
+    cfg = sc.cfg
+    pre = Scenario(cfg, sc.max_seq, n_rows, seed=seed, with_q=False)
+    pre.kv_k, pre.kv_v = sc.kv_k, sc.kv_v
+    pre.oracle_writeback(il, 0)
+    rng = np.random.default_rng(seed + 1)
+    rows = rng.choice(n_rows, size=max(1, int(n_rows * frac)), replace=False)
+    big = Scenario(cfg, sc.max_seq, 1, seed=0, with_q=False)
+    big.w_norms = np.concatenate([pre.w_norms, np.full(128, np.float16(8.0)).view(np.uint16)])
+    big.kv_k, big.kv_v = sc.kv_k, sc.kv_v
+    for r in rows:
+        big.act[big.k_off:big.k_off + cfg.kv_dim] = pre.act[pre.k_off + r * cfg.kv_dim:
+                                                            pre.k_off + (r + 1) * cfg.kv_dim]
+        big.act[big.v_off:big.v_off + cfg.kv_dim] = pre.act[pre.v_off + r * cfg.kv_dim:
+                                                            pre.v_off + (r + 1) * cfg.kv_dim]
+        big.oracle_writeback(il, int(r), m=1, w_k_off=256)
+    return rows

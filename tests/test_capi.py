@@ -66,6 +66,18 @@ def test_config_validation_before_device():
         bp.Model(layout.Config(), 0)
 
 
+def test_max_seq_guard_for_32bit_layer_offsets():
+    # The kernels address rows inside one layer with 32-bit offsets
+    # (row * kv_dim + column), so max_seq * kv_dim must fit in 2^32; the check
+    # runs before any device query, so it is a Config error on any host.
+    kv_dim = 1024
+    limit = (1 << 32) // kv_dim          # 4,194,304 rows: exactly 2^32 bytes per layer
+    with pytest.raises(bp.ConfigError, match="32-bit"):
+        bp.Model(layout.Config(n_layer=1), limit + 1)
+    with pytest.raises(bp.ConfigError, match="32-bit"):
+        bp.Model(layout.Config(n_layer=1, n_head=64, n_kv_head=16), limit // 2 + 1)
+
+
 def test_no_device_maps_to_no_adapter():
     import torch
     if torch.cuda.is_available():

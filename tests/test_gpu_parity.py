@@ -10,7 +10,7 @@ import pytest
 
 import oracle as orc
 from bonsai_pot_amd import layout
-from helpers import DeviceScenario, Scenario, assert_attn_close
+from helpers import DeviceScenario, Scenario, assert_attn_close, write_outlier_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -265,3 +265,46 @@ def test_fused_decode_step_sequence(cuda):
             assert_attn_close(dev.out_f32(1)[0], want, f"step {step} layer {il}")
     k, v = dev.kv_host()
     assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v)
+
+
+@pytest.mark.parametrize("hpw", ["1", "2"])
+@pytest.mark.parametrize("m,pos_base", [(512, 0), (200, 900)])
+def test_prefill_with_outlier_key_rows(cuda, monkeypatch, m, pos_base, hpw):
+    """Causal prefill over a cache whose K rows are 1 % x8 (rows of the chunk
+    itself and of the cached prefix): scores far above the running max drive
+    the lazy rescale with P up to 2^8 in f16. The cache [0, pos_base + m) is
+    written by the oracle; the device runs the attention only."""
+    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw)
+    _say(f"[prefill-outliers] m={m} pos_base={pos_base} heads_per_wave={hpw}")
+    cfg = layout.Config(n_layer=2)
+    sc = Scenario(cfg, max_seq=pos_base + m + 1, m_tokens=m, seed=1300 + m + pos_base)
+    write_outlier_rows(sc, 1, pos_base + m, seed=1400 + m)
+    sc.oracle_q_norm_rope(pos_base)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.attention(1, pos_base, is_prefill=True)
+    want = sc.oracle_attention(1, pos_base, is_prefill=True)
+    assert_attn_close(dev.out_f32(), want, f"prefill outliers m={m} pos={pos_base} hpw={hpw}")
+
+
+def test_config1_real_cache_last_layer(cuda):
+    """configs[1]'s real cache: n_layer 36, ctx 4096, the fused step on the last
+    layer (35). Cache rows written by the oracle for layer 35 only; after the
+    step layer 35 gains row 4096 and every other layer's bytes are untouched."""
+    _say("[config1] n_layer=36 ctx=4096 layer 35")
+    cfg = layout.Config(n_layer=36)
+    pos = 4096
+    sc = Scenario(cfg, max_seq=pos + 64, m_tokens=1, seed=4135)
+    pre = Scenario(cfg, pos + 64, pos, seed=4136, with_q=False)
+    pre.kv_k, pre.kv_v = sc.kv_k, sc.kv_v
+    pre.oracle_writeback(35, 0)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.decode_step(35, pos)
+    sc.oracle_q_norm_rope(pos)
+    sc.oracle_writeback(35, pos)
+    k, v = dev.kv_host()
+    assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v), "cache bytes differ"
+    _, want = sc.oracle_decode(35, pos)
+    assert_attn_close(dev.out_f32(1)[0], want, "config1 layer 35 decode step")
+    # and the plain decode entry point on the same cache
+    dev.decode(35, pos)
+    assert_attn_close(dev.out_f32(1)[0], want, "config1 layer 35 decode")

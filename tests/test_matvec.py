@@ -188,8 +188,9 @@ def test_oracle_silu_and_normed_vs_f64():
 
 # ---------------------------------------------------------------- GPU: HIP vs oracle
 # Two arithmetics (BP_MATVEC_ARITH, read at model creation):
-#  * "f16": the reference's f16 sums in its order -> bit-exact with the oracle;
-#  * "mfma" (default): x rounded to 15 bits of each block's max |x|, exact
+#  * "f16" (default): the reference's f16 sums in its order -> bit-exact with
+#    the oracle;
+#  * "mfma" (opt-in): x rounded to 15 bits of each block's max |x|, exact
 #    integer sums, f32 scaling -> within the bound of _mfma_bound of the exact
 #    f64 product of the staged x, and within that bound plus the oracle's own
 #    f16-accumulation bound of the oracle. "mfma_stream" forces the MFMA
@@ -365,13 +366,18 @@ def test_matvec_fused_normed(cuda, monkeypatch, arith, ranges):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("min_tiles,want_exact", [("2048", True), ("1", False)])
-def test_matvec_auto_dispatch(cuda, monkeypatch, min_tiles, want_exact):
-    """Default arithmetic: the f16-order kernel (bit-exact) below the streaming
-    size, the MFMA kernel from it on."""
+@pytest.mark.parametrize("arith,min_tiles,want_exact", [(None, "2048", True), (None, "1", True),
+                                                        ("auto", "2048", True), ("auto", "1", False)])
+def test_matvec_default_and_auto_dispatch(cuda, monkeypatch, arith, min_tiles, want_exact):
+    """Default arithmetic: the f16-order kernel (the reference's bits) at every
+    size. "auto": the f16-order kernel below the streaming size, the MFMA
+    kernel from it on."""
     import torch
     from bonsai_pot_amd import Model, layout
-    monkeypatch.delenv("BP_MATVEC_ARITH", raising=False)
+    if arith is None:
+        monkeypatch.delenv("BP_MATVEC_ARITH", raising=False)
+    else:
+        monkeypatch.setenv("BP_MATVEC_ARITH", arith)
     monkeypatch.setenv("BP_MATVEC_STREAM_MIN_TILES", min_tiles)
     n, k = 512, 2560
     rng = np.random.default_rng(5)

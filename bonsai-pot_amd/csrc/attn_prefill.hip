@@ -56,13 +56,40 @@ constexpr int kChunk = 64;               // cache rows per LDS chunk
 constexpr int kSub = kChunk / 16;        // 16-row S^T sub-tiles per chunk
 constexpr int kKHalves = kChunk * kHeadDim;   // K rows, 256 B each
 constexpr int kVHalves = kHeadDim * kChunk;   // V^T rows (dims), 128 B each
-constexpr int kBufHalves = kKHalves + kVHalves;   // one staged chunk (32 KB)
+constexpr int kLBytes = kChunk * kHeadDim;    // fp8 K residual rows, 128 B each
+constexpr int kBufHalves = kKHalves + kVHalves + kLBytes / 2;   // one staged chunk (40 KB)
+// The K residual is stored as fp8 of 2^11 (k - f16(k)); the q.k correction
+// MFMA scales its product back by 2^-11 (E8M0 exponent 127 - 11).
+constexpr int kResidShift = 11;
+constexpr int kResidScaleE8M0 = 127 - kResidShift;
+constexpr int kOneE8M0 = 127;
 constexpr float kLazy = 8.0f;            // lazy-rescale threshold (log2 units)
 
 struct alignas(16) U4 { uint32_t w[4]; };
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// c + 2^-11 (a . b) over 128 k of fp8 (e4m3) operands: the q.k correction by
+// the K residual. Lane l holds 32 k-values of row / column l % 16 in each
+// operand, the same k set for A and B, so the product pairs them whatever
+// order the hardware walks k in.
+__device__ __forceinline__ f32x4 mfma_resid(i32x8 a, i32x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, kResidScaleE8M0, 0, kOneE8M0);
+}
+// Two floats -> two e4m3 bytes (round to nearest even) in half kHi of `old`.
+// Inputs are clamped to the format's +-448 first (out-of-range values would
+// otherwise convert to NaN).
+template <bool kHi>
+__device__ __forceinline__ int pack_fp8(float a, float b, int old) {
+    a = fminf(fmaxf(a, -448.0f), 448.0f);
+    b = fminf(fmaxf(b, -448.0f), 448.0f);
+    return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, old, kHi);
+}
+// Four floats -> four e4m3 bytes (little-endian order).
+__device__ __forceinline__ int pack4_fp8(float a, float b, float c, float d) {
+    return pack_fp8<true>(c, d, pack_fp8<false>(a, b, 0));
 }
 
 // Position of chunk row `key` (0..63) along the MFMA k axis of the PV step:
@@ -83,6 +110,10 @@ __device__ __forceinline__ int k_addr(int row, int group) {
 __device__ __forceinline__ int v_addr(int dim, int group) {
     return dim * kChunk + 8 * (group ^ (dim & 7));
 }
+// Byte address of 16-byte group j of K-residual row r: j ^ (r & 7).
+__device__ __forceinline__ int l_addr(int row, int group) {
+    return row * kHeadDim + 16 * (group ^ (row & 7));
+}
 
 // Maximum across the 4 lane groups of a token column (lanes l, l^16, l^32,
 // l^48), by lane-row swaps (no LDS round trip).
@@ -99,11 +130,11 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 // Dequantization pass: one 256-thread workgroup per (64-row chunk, KV head)
-// writes the chunk's f16 K rows and its V^T (dims x slots, keys in v_slot
-// order) to the image, zeros past n_rows. Values are f16(d * q), computed as
-// in the decode path: byte (q xor 0x80) under exponent byte 0x64 is the exact
-// f16 value 1152 + q, and fma(1152 + q, d, -1152 d) is rounded to f16 once.
-//  K: thread t -> row t >> 2, Q8_0 block t & 3 (32 dims, 64 bytes out).
+// writes the chunk's K rows (f16 and fp8 residual) and its V^T (dims x slots,
+// keys in v_slot order) to the image, zeros past n_rows. Each value is the
+// reference's f32 d * q; K keeps f16(k) plus e4m3(2^11 (k - f16(k))), V
+// keeps f16(v).
+//  K: thread t -> row t >> 2, Q8_0 block t & 3 (32 dims: 64 + 32 bytes out).
 //  V: thread t -> rows 4 (t >> 4) .. +3, dims 8 (t & 15) .. +7; each dim's 4
 //     values are 4 consecutive V^T slots, one 8-byte LDS write.
 __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
@@ -133,42 +164,48 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
         if (row > last) vd[i] = 0.0f;
     }
     if (krow > last) kd = 0.0f;
-    auto deq = [](uint32_t x, uint32_t sel, float d, float cc) {   // x already xor 0x80808080
-        const f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, sel));
-        const f16x2 r = {static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.x), d, cc)),
-                         static_cast<_Float16>(__builtin_fmaf(static_cast<float>(h.y), d, cc))};
-        return __builtin_bit_cast(uint32_t, r);
-    };
-    // ---- K rows ----
+    // ---- K rows: f16 value and fp8 residual of k = d * q (f32, as the
+    // reference dequantizes) ----
     {
-        const float kc = -1152.0f * kd;
         uint32_t w[16];
+        int lo[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const uint32_t x = (i < 4 ? kq0.w[i] : kq1.w[i - 4]) ^ 0x80808080u;
-            w[2 * i] = deq(x, 0x04010400u, kd, kc);
-            w[2 * i + 1] = deq(x, 0x04030402u, kd, kc);
+            const uint32_t x = i < 4 ? kq0.w[i] : kq1.w[i - 4];
+            float k[4], r[4];
+            _Float16 h[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                k[e] = kd * static_cast<float>(static_cast<int8_t>(x >> (8 * e)));
+                h[e] = static_cast<_Float16>(k[e]);
+                r[e] = (k[e] - static_cast<float>(h[e])) * static_cast<float>(1 << kResidShift);
+            }
+            w[2 * i] = __builtin_bit_cast(uint32_t, f16x2{h[0], h[1]});
+            w[2 * i + 1] = __builtin_bit_cast(uint32_t, f16x2{h[2], h[3]});
+            lo[i] = pack4_fp8(r[0], r[1], r[2], r[3]);
         }
         uint16_t* kdst = a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves;
 #pragma unroll
         for (int i = 0; i < 4; i++)
             *reinterpret_cast<U4*>(kdst + k_addr(kr, 4 * kb + i)) = U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
-    }
-    // ---- V^T through LDS ----
-    {
-        float vc[4];
+        uint8_t* ldst = a.kl8 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kLBytes;
 #pragma unroll
-        for (int i = 0; i < 4; i++) vc[i] = -1152.0f * vd[i];
+        for (int i = 0; i < 2; i++)
+            *reinterpret_cast<U4*>(ldst + l_addr(kr, 2 * kb + i)) =
+                U4{{static_cast<uint32_t>(lo[4 * i]), static_cast<uint32_t>(lo[4 * i + 1]),
+                    static_cast<uint32_t>(lo[4 * i + 2]), static_cast<uint32_t>(lo[4 * i + 3])}};
+    }
+    // ---- V^T through LDS: f16(d * q) ----
+    {
         const int slot = v_slot(4 * vq4);   // rows 4 vq4 .. +3 -> slots slot .. slot + 3
 #pragma unroll
         for (int e = 0; e < 8; e++) {   // dim 8 vdg + e
             uint16_t hv[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t word = (e < 4 ? vq[i].x : vq[i].y) ^ 0x80808080u;
-                const uint32_t sel = 0x04040400u | static_cast<uint32_t>(e & 3);
-                const _Float16 x = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, word, sel)).x;
-                hv[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__builtin_fmaf(static_cast<float>(x), vd[i], vc[i])));
+                const uint32_t word = e < 4 ? vq[i].x : vq[i].y;
+                const float v = vd[i] * static_cast<float>(static_cast<int8_t>(word >> (8 * (e & 3))));
+                hv[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
             }
             *reinterpret_cast<uint2*>(&vt[8 * vdg + e][slot]) =
                 make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16), hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
@@ -191,7 +228,8 @@ template <int kHpw>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     constexpr int kHeadsPerWave = kHpw;
     constexpr int kHeadSets = 2 / kHpw;
-    // lds[stream][buf]: staged chunk (K rows then V^T rows), 2 streams x 2 buffers.
+    // lds[stream][buf]: staged chunk (K rows, V^T rows, K residual rows), 2
+    // streams x 2 buffers (160 KB, all of the CU's LDS).
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
 
     const int t = threadIdx.x;
@@ -224,6 +262,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     uint32_t wtok0 = 0, my_tok = 0, my_kend = 0, wave_kend = 0;
     bool unit_live = false;
     f16x8 qb[kHeadsPerWave][4];
+    i32x8 q8[kHeadsPerWave];   // q of token my_tok, dims 32 lg .. +32, as e4m3 (residual MFMA)
     f32x4 o[kHeadsPerWave][8];
     float m_run[kHeadsPerWave], l_run[kHeadsPerWave];
     f32x4 l_acc[kHeadsPerWave];   // row sums of P (every element holds the token's sum)
@@ -244,6 +283,22 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
                     raw = *reinterpret_cast<const U4*>(a.q + static_cast<uint64_t>(my_tok) * a.q_stride +
                                                        (h0 + h) * kHeadDim + 32 * kk + 8 * lg);
                 qb[h][kk] = __builtin_bit_cast(f16x8, raw);
+            }
+            {
+                U4 raw[4] = {};
+                if (unit_live && my_tok < a.m_tokens) {
+                    const uint16_t* qp = a.q + static_cast<uint64_t>(my_tok) * a.q_stride + (h0 + h) * kHeadDim + 32 * lg;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) raw[i] = *reinterpret_cast<const U4*>(qp + 8 * i);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const f16x8 v = __builtin_bit_cast(f16x8, raw[i]);
+                    q8[h][2 * i] = pack4_fp8(static_cast<float>(v[0]), static_cast<float>(v[1]),
+                                             static_cast<float>(v[2]), static_cast<float>(v[3]));
+                    q8[h][2 * i + 1] = pack4_fp8(static_cast<float>(v[4]), static_cast<float>(v[5]),
+                                                 static_cast<float>(v[6]), static_cast<float>(v[7]));
+                }
             }
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -273,20 +328,23 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // the second half of it); B waves on tile B.
     start_unit(is_b || n_a == 0 ? tile_b : tile_a);
 
-    // ---- staging: a chunk's K rows and V^T (32 KB, already swizzled in the
-    // image) copied straight into LDS by global_load_lds (no registers): wave
-    // w's copy k (0..3) moves 1 KB, pieces 512 k + 64 w + lane. -------------------
+    // ---- staging: a chunk's K rows, V^T and K residual (40 KB, already
+    // swizzled in the image) copied straight into LDS by global_load_lds (no
+    // registers): wave w's copy k (0..4) moves 1 KB, pieces 512 k + 64 w + lane
+    // (K: k = 0, 1; V^T: k = 2, 3; residual: k = 4). -------------------------------
     const uint16_t* k16 = a.k16 + static_cast<uint64_t>(g) * a.ws_chunks * kKHalves;
     const uint16_t* vt16 = a.vt16 + static_cast<uint64_t>(g) * a.ws_chunks * kVHalves;
+    const uint8_t* kl8 = a.kl8 + static_cast<uint64_t>(g) * a.ws_chunks * kLBytes;
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     auto load_chunk = [&](uint16_t* buf, uint32_t c) {
         const uint16_t* ks = k16 + static_cast<uint64_t>(c) * kKHalves;
         const uint16_t* vs = vt16 + static_cast<uint64_t>(c) * kVHalves;
+        const uint16_t* ls = reinterpret_cast<const uint16_t*>(kl8 + static_cast<uint64_t>(c) * kLBytes);
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int piece = 512 * (k & 1) + 64 * wv;   // 16-byte pieces within K or V^T
-            const uint16_t* src = (k < 2 ? ks : vs) + 8 * (piece + lane);
-            uint16_t* dst = buf + (k < 2 ? 0 : kKHalves) + 8 * piece;
+        for (int k = 0; k < 5; k++) {
+            const int piece = 512 * (k & 1) + 64 * wv;   // 16-byte pieces within K, V^T or residual
+            const uint16_t* src = (k < 2 ? ks : k < 4 ? vs : ls) + 8 * ((k < 4 ? piece : 64 * wv) + lane);
+            uint16_t* dst = buf + (k < 2 ? 0 : k < 4 ? kKHalves : kKHalves + kVHalves) + 8 * (k < 4 ? piece : 64 * wv);
             __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
                                              (void __attribute__((address_space(3)))*)dst, 16, 0, 0);
         }
@@ -299,6 +357,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
         if (!unit_live || key0 >= wave_kend) { issue(); return; }
         const uint16_t* kb = buf;
         const uint16_t* vb = buf + kKHalves;
+        const uint8_t* lb = reinterpret_cast<const uint8_t*>(buf + kKHalves + kVHalves);
         // S^T = K Q^T, k-step outer: each step issues 8 independent MFMAs.
         f32x4 s[kHeadsPerWave][kSub];
 #pragma unroll
@@ -315,6 +374,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             for (int st2 = 0; st2 < kSub; st2++)
 #pragma unroll
                 for (int h = 0; h < kHeadsPerWave; h++) s[h][st2] = mfma16(ka[st2], qb[h][kk], s[h][st2]);
+        }
+        // Residual correction: s += 2^-11 (K residual . q) on the fp8 matrix
+        // path, one 128-deep MFMA per sub-tile and head.
+#pragma unroll
+        for (int st2 = 0; st2 < kSub; st2++) {
+            const int row = 16 * st2 + lr;
+            const U4 r0 = *reinterpret_cast<const U4*>(lb + l_addr(row, 2 * lg));
+            const U4 r1 = *reinterpret_cast<const U4*>(lb + l_addr(row, 2 * lg + 1));
+            const i32x8 ra = {static_cast<int>(r0.w[0]), static_cast<int>(r0.w[1]), static_cast<int>(r0.w[2]),
+                              static_cast<int>(r0.w[3]), static_cast<int>(r1.w[0]), static_cast<int>(r1.w[1]),
+                              static_cast<int>(r1.w[2]), static_cast<int>(r1.w[3])};
+#pragma unroll
+            for (int h = 0; h < kHeadsPerWave; h++) s[h][st2] = mfma_resid(ra, q8[h], s[h][st2]);
         }
         issue();
         // Mask (only chunks that reach past the unit's earliest visible row);
@@ -353,7 +425,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++) {
                 const float m_new = up[h] ? cm[h] : m_run[h];
-                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - m_new);   // 0 from -inf, 1 if kept
+                // 0 from -inf, 1 if kept (also for a row whose max is still
+                // -inf, where the difference would be NaN)
+                const float alpha = up[h] ? __builtin_amdgcn_exp2f(m_run[h] - m_new) : 1.0f;
                 m_run[h] = m_new;
                 l_acc[h][0] *= alpha;   // only element 0 is read
 #pragma unroll
@@ -367,7 +441,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             f16x8 pb[kHeadsPerWave];
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++) {
-                const float neg_m = -m_run[h];
+                // m_run is still -inf only if every score of the token so far
+                // is masked (a second-half unit whose first chunk lies past
+                // the token's last row): then p = exp2(-inf) = 0, not NaN.
+                const float neg_m = m_run[h] == -INFINITY ? 0.0f : -m_run[h];
                 float p[8];
 #pragma unroll
                 for (int half = 0; half < 2; half++)

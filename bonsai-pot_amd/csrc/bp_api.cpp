@@ -39,7 +39,7 @@ struct bp_model {
     uint16_t* rope_cs;
     float* partials;
     uint64_t partials_floats;
-    uint16_t* kv16;       // prefill: f16 image of one layer's K and V (prefill_image_bytes)
+    uint16_t* kv16;       // prefill: image of one layer's K and V (prefill_image_bytes)
     uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
@@ -513,8 +513,10 @@ bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t
     }
     a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:524
     a.ws_chunks = (m->max_seq + 63) / 64;
+    const uint64_t image_elems = static_cast<uint64_t>(m->cfg.n_kv_head) * a.ws_chunks * 64 * 128;
     a.k16 = m->kv16;
-    a.vt16 = m->kv16 + bp::prefill_image_bytes(m->cfg.n_kv_head, m->max_seq) / 4;
+    a.vt16 = m->kv16 + image_elems;
+    a.kl8 = reinterpret_cast<uint8_t*>(m->kv16 + 2 * image_elems);
     a.n_rows = static_cast<uint32_t>(rows);
     return hip_check(m, bp::launch_prefill(a, m->cfg.n_kv_head, m->stream), "attention launch");
 }

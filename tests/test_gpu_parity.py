@@ -140,11 +140,13 @@ def test_decode_ctx32k_with_outlier_rows(cuda):
 
 
 @pytest.mark.parametrize("m,pos_base", [(1, 0), (17, 0), (64, 0), (65, 0), (100, 5), (512, 0),
-                                        (130, 1000), (33, 31)])
+                                        (130, 1000), (33, 31), (200, 900)])
 @pytest.mark.parametrize("hpw", ["1", "2"])
 def test_prefill_vs_oracle(cuda, monkeypatch, m, pos_base, hpw):
     """Both prefill_kernel layouts (1 or 2 query heads per wave; by default the
-    grid size picks one), forced through BP_PREFILL_HEADS_PER_WAVE."""
+    grid size picks one), forced through BP_PREFILL_HEADS_PER_WAVE. (200, 900)
+    gives second-half units whose first chunk lies wholly past some tokens'
+    last row (all scores masked while the running max is still unset)."""
     monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw)
     _say(f"[prefill] m={m} pos_base={pos_base} heads_per_wave={hpw}")
     cfg = layout.Config(n_layer=2)

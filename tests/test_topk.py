@@ -7,8 +7,9 @@ network's tie handling: for distinct logits the result is the sorted top-k
 -1e30; with ties the values are still the sorted top-k multiset and every
 index names a logit of that value, each index once. Which of several equal
 logits is returned (and in which order) is fixed only by the reference's
-network, which the oracle restates step by step; that part has no
-independent pin.
+network; tests/test_topk_wgsl_sim.py pins the oracle's restatement of it
+against a second, separately written workgroup simulation of the shader on
+tie-heavy inputs.
 
 GPU part: the HIP kernels through the C ABI against the oracle, values and
 indices identical, ties included.

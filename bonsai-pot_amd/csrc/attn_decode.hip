@@ -63,7 +63,16 @@ template <int kH> struct SplitShape {
     static constexpr int kRowSets = kWaves / kH;
     static constexpr int kWgPerCu = 8 / kWaves;   // at 2 waves per SIMD
 };
-constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, pad (16-byte aligned rows)
+// Split-K partials of one launch (n_head query heads, ns splits): the o rows
+// first, [n_head][ns][128] f32 (512-byte rows, so a 32-dim piece is one whole
+// 128-byte line), then the (m, l) pairs, [n_head][ns][2] f32.
+constexpr int kPartStride = kHeadDim + 2;  // floats per (head, split) partial
+__device__ __forceinline__ float* part_o(float* base, uint32_t h, uint32_t ns, uint32_t s) {
+    return base + (static_cast<uint64_t>(h) * ns + s) * kHeadDim;
+}
+__device__ __forceinline__ float* part_ml(float* base, uint32_t n_head, uint32_t h, uint32_t ns, uint32_t s) {
+    return base + static_cast<uint64_t>(n_head) * ns * kHeadDim + (static_cast<uint64_t>(h) * ns + s) * 2;
+}
 constexpr int kMaxSplits = 128;          // the merge pass holds (m, l) of splits lane, lane + 64
 constexpr uint32_t kExp64 = 0x64646464u;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -396,10 +405,12 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
                 static_cast<uint32_t>(f2h(o[k] * inv_l)) | (static_cast<uint32_t>(f2h(o[k + 1] * inv_l)) << 16);
         return;
     }
-    float* part = a.partials + (static_cast<uint64_t>(qhd) * a.n_splits + split) * kPartStride;
+    float* part = part_o(a.partials, qhd, a.n_splits, split);
 #pragma unroll
     for (int k = 0; k < kE; k += 2) *reinterpret_cast<float2*>(part + fd + k) = make_float2(o[k], o[k + 1]);
-    if (t % kTpH == 0) *reinterpret_cast<float2*>(part + kHeadDim) = make_float2(M, L);
+    if (t % kTpH == 0)
+        *reinterpret_cast<float2*>(part_ml(a.partials, a.kv_dim / kHeadDim * kGroup, qhd, a.n_splits, split)) =
+            make_float2(M, L);
 }
 
 // One wave per (query head, 32-dim chunk); kLoads = 8 (up to 64 splits) or
@@ -410,7 +421,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
     const uint32_t h = blockIdx.x >> 2, c = blockIdx.x & 3;
     const uint32_t g = h / kGroup;
     const uint32_t ns = a.n_splits;
-    const float* ph = a.partials + static_cast<uint64_t>(h) * ns * kPartStride;
+    const float* ph = part_o(a.partials, h, ns, 0);
+    const float* pml = part_ml(a.partials, a.kv_dim / kHeadDim * kGroup, h, ns, 0);
     const float c2 = a.scale * kLog2e;
 
     // O chunk loads: lane -> splits (lane >> 3) + 8i, dims 32c + 4 (lane & 7) .. +3.
@@ -419,13 +431,13 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < kLoads; i++) {
         const uint32_t s = min(static_cast<uint32_t>((lane >> 3) + 8 * i), ns - 1);
-        ov[i] = *reinterpret_cast<const float4*>(ph + static_cast<uint64_t>(s) * kPartStride + 32 * c + 4 * f4);
+        ov[i] = *reinterpret_cast<const float4*>(ph + static_cast<uint64_t>(s) * kHeadDim + 32 * c + 4 * f4);
     }
     // (m, l) of splits lane and lane + 64.
     const uint32_t ls0 = min(static_cast<uint32_t>(lane), ns - 1), ls1 = min(static_cast<uint32_t>(lane) + 64u, ns - 1);
-    const float2 ml0 = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls0) * kPartStride + kHeadDim);
+    const float2 ml0 = *reinterpret_cast<const float2*>(pml + 2 * ls0);
     float2 ml1 = make_float2(-INFINITY, 0.0f);
-    if constexpr (kLoads > 8) ml1 = *reinterpret_cast<const float2*>(ph + static_cast<uint64_t>(ls1) * kPartStride + kHeadDim);
+    if constexpr (kLoads > 8) ml1 = *reinterpret_cast<const float2*>(pml + 2 * ls1);
     const float m_s0 = static_cast<uint32_t>(lane) < ns ? ml0.x : -INFINITY;
     const float m_s1 = static_cast<uint32_t>(lane) + 64u < ns ? ml1.x : -INFINITY;
 

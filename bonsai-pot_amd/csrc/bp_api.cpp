@@ -731,12 +731,12 @@ static bp_status snapshot_copy(bp_model* m, uint32_t pos, uint8_t* payload, uint
 // ---- allocation-free decode ---------------------------------------------------
 // Split-K partials for bp_attention_decode_noalloc live in this file-scope
 // device array instead of memory the library allocates: 64 query heads x 128
-// splits (the most decode_plan makes) x 132 floats per partial = 4.125 MiB, so
+// splits (the most decode_plan makes) x 130 floats per partial = 4.0625 MiB, so
 // every context fits at n_head <= 64. Every GPU holds its own copy until the
 // process ends.
 // In host code `scratch` is only a stand-in for the symbol: kernels get the
 // device address from hipGetSymbolAddress, looked up once per device.
-constexpr uint64_t kNoAllocScratchFloats = 64ull * 128 * 132;
+constexpr uint64_t kNoAllocScratchFloats = 64ull * 128 * 130;
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 constexpr int kNoAllocMaxDevices = 64;

@@ -56,7 +56,7 @@ struct DecodeArgs {
     const uint16_t* q;        // act + q_off: [n_head][128] (raw, un-normalized q when fused)
     uint16_t* out;            // act + out_off: [n_head][128]
     KvView k, v;              // layer bases
-    float* partials;          // [n_head][n_splits][decode_partial_stride()]
+    float* partials;          // n_head * n_splits * decode_partial_stride() floats: o rows, then (m, l)
     uint32_t kv_dim;
     uint32_t n_rows;          // rows streamed by the split pass: [0, n_rows)
     uint32_t split_len;       // rows per workgroup, multiple of 32

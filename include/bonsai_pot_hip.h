@@ -231,7 +231,7 @@ bp_status bp_debug_lose_device(bp_model* model);
  * `layer_il`, q already normalized at act[q_off], output at act[out_off] —
  * but it needs no bp_model: the caller passes its own kv_k / kv_v buffers (the
  * reference byte layout for cfg->n_layer x max_seq), and the split-K partials
- * live in a fixed 4.125 MiB device array inside the library (one per GPU, kept
+ * live in a fixed 4.0625 MiB device array inside the library (one per GPU, kept
  * until the process ends), so the call never allocates. Launches on `stream`
  * on the current device. BP_ERR_CONFIG when n_head x the split count of
  * pos + 1 rows does not fit that array (it fits every context at n_head <= 64).

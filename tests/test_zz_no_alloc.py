@@ -51,7 +51,7 @@ def test_noalloc_decode_matches_model_decode(cuda):
         _, want = sc.oracle_decode(il, pos)
         assert_attn_close(got_bits.view(np.float16).astype(np.float32), want, f"noalloc decode pos {pos}")
     # rejected before any launch: n_head * splits beyond the fixed array
-    # (4096 KV heads: one split each, 16384 x 132 floats > 64 x 128 x 132)
+    # (4096 KV heads: one split each, 16384 x 130 floats > 64 x 128 x 130)
     big = _Config(1, 16384, 4096, 128, 1e-6, 1e6)
     rc = bp.lib.bp_attention_decode_noalloc(ctypes.byref(big), dev.kv_k, dev.kv_v, 64, a, 0, 0, 0, 10, stream)
     assert rc == errors.BP_ERR_CONFIG and b"scratch" in bp.lib.bp_last_error()

@@ -193,6 +193,17 @@ def bench_decode(torch, args, ctx, n_layer, graph_ok=True):
         "kernel_bytes": kbytes, "kernel_GBps": kbytes / (avg_us * 1e-6) / 1e9,
     }
     res["kernel_frac_hbm"] = res["kernel_GBps"] / HBM_PEAK_GBS
+    if graph_ok and not args.no_graph:
+        # The graph floor of the step's shape: two back-to-back launches per
+        # layer of a one-thread kernel (an in-place add on one element), in a
+        # graph of the same 2 x n_layer nodes. The step cannot go below it
+        # with two launches per layer.
+        one = torch.zeros(1, device="cuda")
+        gf = make_graph(torch, b, lambda: [one.add_(1.0) for _ in range(2 * n_layer)])
+        floor_s = time_region(torch, gf.replay, args.steps, args.warmup)
+        res["launch_floor_us_per_layer"] = floor_s * 1e6 / n_layer
+        res["us_per_layer"] = step_s * 1e6 / n_layer
+        res["launch_floor_share"] = floor_s / step_s
     b.model.close()
     return res, step_bytes
 

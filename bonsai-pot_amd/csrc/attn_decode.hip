@@ -157,8 +157,10 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t rr = min(r0 + 4u * lg + j, row_last);
-            B.kd[j] = a.k.d[rr * nb_row + dcol];
-            B.vd[j] = a.v.d[rr * nb_row + dcol];
+            // byte offsets in 32 bits: base (SGPRs) + one VGPR offset per load
+            const uint32_t doff = (rr * nb_row + dcol) * 4u;
+            B.kd[j] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.k.d) + doff);
+            B.vd[j] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v.d) + doff);
             B.vv[j] = *reinterpret_cast<const u32x2*>(a.v.qs + (rr * kv_dim + vcol));
         }
     };

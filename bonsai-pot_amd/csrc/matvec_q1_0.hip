@@ -79,25 +79,33 @@ struct WTile {
 };
 
 // Tile t of a workgroup: rows 8 (t / tcols) .. + 7, blocks 4 (t % tcols) .. + 3;
-// lane = (row slot lane >> 3, block (lane >> 1) & 3, half lane & 1).
-struct TileLane {
-    uint32_t r, b;
+// lane = (row slot lane >> 3, block (lane >> 1) & 3, half lane & 1). A wave
+// walks tiles wave, wave + n_wave, ...; it keeps the tile's (row group, block
+// group) in scalar registers and steps them without a division.
+struct TilePos {
+    uint32_t tile, rq, col;   // wave-uniform
 };
-__device__ __forceinline__ TileLane tile_lane(uint32_t tile, uint32_t tcols, int lane) {
-    return {(tile / tcols) * 8 + (lane >> 3), (tile % tcols) * 4 + ((lane >> 1) & 3)};
+__device__ __forceinline__ void tile_step(TilePos& p, uint32_t n_wave, uint32_t tcols) {
+    p.tile += n_wave;
+    p.col += n_wave;
+    while (p.col >= tcols) {
+        p.col -= tcols;
+        ++p.rq;
+    }
 }
 
-__device__ __forceinline__ WTile load_tile(const MatvecArgs& a, uint32_t tile, uint32_t n_tiles, uint32_t tcols,
-                                           uint32_t nb, uint32_t n_here, uint32_t rbase, uint32_t d_off,
-                                           uint32_t qs_off, int lane) {
-    WTile w{};
-    const TileLane tl = tile_lane(tile, tcols, lane);
-    w.ok = tile < n_tiles && tl.r < n_here && tl.b < nb;
-    if (w.ok) {
-        const uint64_t rb = static_cast<uint64_t>(rbase + tl.r) * nb + tl.b;
-        w.q = *reinterpret_cast<const uint4*>(a.weights + qs_off + 16 * rb);
-        w.d = *reinterpret_cast<const uint16_t*>(a.weights + d_off + 2 * rb);
-    }
+// Weights of one lane's (row, block) in a tile. Loads are unconditional (the
+// row and block clamped into range), so no lane branches around them; `ok`
+// says whether the lane's (row, block) exists.
+__device__ __forceinline__ WTile load_tile(const MatvecArgs& a, const TilePos& p, uint32_t n_tiles, uint32_t nb,
+                                           uint32_t n_here, uint32_t rbase, uint32_t d_off, uint32_t qs_off, int lane) {
+    WTile w;
+    const uint32_t r = p.rq * 8 + (lane >> 3), b = p.col * 4 + ((lane >> 1) & 3);
+    w.ok = p.tile < n_tiles && r < n_here && b < nb;
+    const uint32_t rc = min(r, n_here - 1), bc = min(b, nb - 1);
+    const uint32_t rb = (rbase + rc) * nb + bc;
+    w.q = *reinterpret_cast<const uint4*>(a.weights + qs_off + 16 * rb);
+    w.d = *reinterpret_cast<const uint16_t*>(a.weights + d_off + 2 * rb);
     return w;
 }
 
@@ -147,8 +155,8 @@ __global__ __launch_bounds__(kMvMaxThreads) void matvec_q1_0_kernel(MatvecArgs a
 
     const uint32_t tcols = (nb + 3) / 4;
     const uint32_t n_tiles = (rows / 8) * tcols;
-    uint32_t tile = wave;
-    WTile cur = load_tile(a, tile, n_tiles, tcols, nb, n_here, rbase, d_off, qs_off, lane);   // in flight during pass 1
+    TilePos pos = {static_cast<uint32_t>(wave), static_cast<uint32_t>(wave) / tcols, static_cast<uint32_t>(wave) % tcols};
+    WTile cur = load_tile(a, pos, n_tiles, nb, n_here, rbase, d_off, qs_off, lane);   // in flight during pass 1
 
     // ---- pass 1: stage x (f16) into LDS, 8 elements at a time --------------------
     float ssq = 0.0f;
@@ -205,21 +213,24 @@ __global__ __launch_bounds__(kMvMaxThreads) void matvec_q1_0_kernel(MatvecArgs a
 
     // ---- pass 2: block terms (weights of the next tile loaded ahead) --------------
     const uint32_t h = lane & 1;
-    for (; tile < n_tiles; tile += n_wave) {
-        const WTile nxt = load_tile(a, tile + n_wave, n_tiles, tcols, nb, n_here, rbase, d_off, qs_off, lane);
-        const TileLane tl = tile_lane(tile, tcols, lane);
+    while (pos.tile < n_tiles) {
+        TilePos nxt_pos = pos;
+        tile_step(nxt_pos, n_wave, tcols);
+        const WTile nxt = load_tile(a, nxt_pos, n_tiles, nb, n_here, rbase, d_off, qs_off, lane);
+        const uint32_t r = pos.rq * 8 + (lane >> 3), b = min(pos.col * 4 + ((lane >> 1) & 3), nb - 1);
         const uint32_t q[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
         // both lanes of a pair are valid or invalid together; a shuffle is
         // executed by all lanes
-        const h2v c = q1_half(q, x_sh + tl.b * kBlockHalves + h * kHalfStride, h);
+        const h2v c = q1_half(q, x_sh + b * kBlockHalves + h * kHalfStride, h);
         const h2v c23 = __builtin_bit_cast(h2v, __shfl_xor(__builtin_bit_cast(int, c), 1));
         if (cur.ok && h == 0) {
             const _Float16 sum = ((c.x + c.y) + c23.x) + c23.y;   // f16 adds, in this order
             float d = static_cast<float>(__builtin_bit_cast(_Float16, cur.d));
             if constexpr (kMode == 2) d = d * inv_rms;
-            terms[tl.r * nb + tl.b] = d * static_cast<float>(sum);
+            terms[r * nb + b] = d * static_cast<float>(sum);
         }
         cur = nxt;
+        pos = nxt_pos;
     }
     __syncthreads();
 

@@ -213,8 +213,8 @@ def _host(t):
 def _model(monkeypatch, arith):
     import torch
     from bonsai_pot_amd import Model, layout
-    monkeypatch.setenv("BP_MATVEC_ARITH", "mfma" if arith.startswith("mfma") else arith)
-    monkeypatch.setenv("BP_MATVEC_STREAM_MIN_TILES", "1" if arith == "mfma_stream" else "2048")
+    monkeypatch.setenv("BP_MATVEC_ARITH", "mfma" if arith.startswith("mfma") else "f16")
+    monkeypatch.setenv("BP_MATVEC_STREAM_MIN_TILES", "1" if arith.endswith("_stream") else "2048")
     m = Model(layout.Config(n_layer=1), 64)
     m.set_stream(torch.cuda.current_stream().cuda_stream)
     return m
@@ -234,7 +234,7 @@ def _mfma_bound(buf, d_off, qs_off, n, k, x, scale=1.0):
 def _check(arith, got, want_oracle, out, n, exact, bound_mfma, bound_oracle, old=None, written=None):
     """got / want_oracle: whole act buffers (uint16); exact / bounds per row;
     written: every (offset, rows) output region of the call (default this one)."""
-    if arith == "f16":
+    if arith.startswith("f16"):
         bad = np.flatnonzero(got != want_oracle)
         assert bad.size == 0, f"{bad.size} f16 outputs differ, first at {bad[:8]}"
         return
@@ -304,7 +304,7 @@ def test_matvec_silu(cuda, monkeypatch, arith, n, k, acc):
     d, _ = _decode(buf, d_off, qs_off, n, k)
     ulp_x = (np.abs(d) * (2.0**-10 * np.abs(x)).reshape(k // 128, 128).sum(-1)[None, :]).sum(-1)
     old = act[out_off:out_off + n].view(np.float16).astype(np.float64) if acc else None
-    if arith == "f16":
+    if arith.startswith("f16"):
         gg = got[out_off:].view(np.float16).astype(np.float64)
         ww = want[out_off:].view(np.float16).astype(np.float64)
         assert np.all(np.abs(gg - ww) <= ulp_x + 2.0**-10 * np.abs(ww) + 1e-6)
@@ -350,7 +350,7 @@ def test_matvec_fused_normed(cuda, monkeypatch, arith, ranges):
     m.dispatch_matvec_q1_0_fused_normed(w_d.data_ptr(), a_d.data_ptr(), n_d.data_ptr(), k, in_off,
                                         w_norm_off, r_list)
     got = _host(a_d)
-    if arith == "f16":
+    if arith.startswith("f16"):
         bad = np.flatnonzero(got != want)
         assert bad.size == 0, f"{bad.size} f16 outputs differ, first at {bad[:8]}"
         return
@@ -396,6 +396,37 @@ def test_matvec_default_and_auto_dispatch(cuda, monkeypatch, arith, min_tiles, w
     exact, _ = _brute(buf, d_off, qs_off, n, k, x)
     _check("mfma", got, want, k, n, exact, _mfma_bound(buf, d_off, qs_off, n, k, x),
            _f16_sum_bound(buf, d_off, qs_off, n, k, x))
+
+
+@pytest.mark.gpu
+def test_matvec_lm_head_default_is_reference_bits(cuda, monkeypatch):
+    """The LM head (151936 x 2560) on the default f16-order kernel: every logit
+    bit-identical to the oracle's f16 sums, and the top-k
+    of those logits identical to the oracle's top-k of the oracle's logits."""
+    import torch
+    from bonsai_pot_amd import Model, layout
+    monkeypatch.delenv("BP_MATVEC_ARITH", raising=False)
+    monkeypatch.delenv("BP_MATVEC_STREAM_MIN_TILES", raising=False)
+    n, k = 151936, HIDDEN
+    _say(f"[matvec] lm head default n={n} k={k}")
+    rng = np.random.default_rng(151936)
+    buf, [(d_off, qs_off)] = _weights(rng, [(n, k)])
+    act = _f16(rng.standard_normal(k + n))
+    p = orc.MatvecParams(k=k, n=n, d_offset=d_off, qs_offset=qs_off, input_offset=0, output_offset=k,
+                         accumulate=0)
+    want = orc.matvec_q1_0(p, buf, act)
+    m = Model(layout.Config(n_layer=1), 64)
+    m.set_stream(torch.cuda.current_stream().cuda_stream)
+    w_d, a_d = _dev(buf), _dev(act)
+    m.dispatch_matvec_q1_0(w_d.data_ptr(), a_d.data_ptr(), k, n, d_off, qs_off, 0, k, False)
+    got = _host(a_d)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} logits differ, first at {bad[:8]}"
+    res = torch.zeros(64, dtype=torch.int32, device="cuda")
+    m.dispatch_topk_reduce(a_d.data_ptr(), res.data_ptr(), n, 32, k, 0)
+    vals, idx = m.wait_topk_readback(res.data_ptr(), 0, 32)
+    ores = orc.topk_reduce(orc.TopKParams(n=n, in_offset=k, out_offset=0, k=32), want, np.zeros(72, np.uint32))
+    assert np.array_equal(idx, ores[32:64]) and np.array_equal(vals.view(np.uint32), ores[:32])
 
 
 @pytest.mark.gpu

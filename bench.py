@@ -193,6 +193,31 @@ def bench_decode(torch, args, ctx, n_layer, graph_ok=True):
         "kernel_bytes": kbytes, "kernel_GBps": kbytes / (avg_us * 1e-6) / 1e9,
     }
     res["kernel_frac_hbm"] = res["kernel_GBps"] / HBM_PEAK_GBS
+    # The streaming-read floor of the same byte count on this GPU: the
+    # library's plain read kernel (bp_debug_read_floor: every 16-byte word
+    # read once, 4 loads in flight per thread, 512 workgroups: the fastest of
+    # 512 / 1024 / 2048 / 4096 / 8192 on the box) over kbytes,
+    # per launch in a graph, rotating over as many buffers as layers so that
+    # (like the decode's rotating layers) the reads come from HBM, not the
+    # 256 MB Infinity Cache. kernel_frac_of_read_floor = floor / (split +
+    # merge time).
+    from bonsai_pot_amd import lib as _lib
+    nbytes16 = kbytes // 16 * 16
+    rd = [torch.ones(nbytes16 // 4, device="cuda", dtype=torch.float32) for _ in range(n_layer)]
+    sink = torch.zeros(1024, device="cuda", dtype=torch.int32)
+
+    class _R:
+        model = b.model
+
+    def _read(i):
+        rc = _lib.bp_debug_read_floor(rd[i % n_layer].data_ptr(), nbytes16, sink.data_ptr(), 512,
+                                      torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    rd_us = per_launch_us(torch, _R, _read, 4 * n_layer)
+    res["read_floor_us"] = rd_us
+    res["read_floor_GBps"] = kbytes / (rd_us * 1e-6) / 1e9
+    res["kernel_frac_of_read_floor"] = rd_us / avg_us
+    del rd
     if graph_ok and not args.no_graph:
         # The graph floor of the step's shape: two back-to-back launches per
         # layer of a one-thread kernel (an in-place add on one element), in a

@@ -85,6 +85,7 @@ _SIGS = {
     "bp_kv_snapshot_apply": (_i32, [_vp, _u32, _vp, _u64]),
     "bp_attention_decode_noalloc": (_i32, [ctypes.POINTER(_Config), _vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32,
                                             _vp]),
+    "bp_debug_read_floor": (_i32, [_vp, _u64, _vp, _u32, _vp]),
     "bp_check_device": (_i32, [_vp]),
     "bp_debug_lose_device": (_i32, [_vp]),
     "bp_last_error": (ctypes.c_char_p, []),

@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "lib", "libbonsai_pot_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
-SOURCES = ["bp_api.cpp", "norm_rope_writeback.hip", "attn_decode.hip", "attn_prefill.hip", "matvec_q1_0.hip", "matvec_q1_0_mfma.hip", "matmul_q1_0_q8_0.hip", "topk_reduce.hip"]
+SOURCES = ["bp_api.cpp", "norm_rope_writeback.hip", "attn_decode.hip", "attn_prefill.hip", "matvec_q1_0.hip", "matvec_q1_0_mfma.hip", "matmul_q1_0_q8_0.hip", "topk_reduce.hip", "read_floor.hip"]
 # Per-source additions: the matmul's MFMA results go straight to VGPRs (the
 # default AGPR form costs one v_accvgpr_read per result element in its f32
 # epilogue).

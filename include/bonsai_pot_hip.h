@@ -242,6 +242,14 @@ bp_status bp_attention_decode_noalloc(const bp_config* cfg, void* kv_k, void* kv
                                       uint32_t q_off, uint32_t out_off, uint32_t layer_il, uint32_t pos,
                                       void* stream);
 
+/* Measurement aid, no counterpart in the reference and not part of the
+ * attention path: reads `bytes` (a multiple of 16) of device memory at `src`
+ * once with independent 16-byte loads over `n_workgroups` workgroups of 256
+ * threads and writes one word per workgroup to `sink` (n_workgroups x 4 bytes),
+ * on `stream`. bench.py times it as the streaming-read floor of a decode's
+ * byte count. */
+bp_status bp_debug_read_floor(const void* src, uint64_t bytes, void* sink, uint32_t n_workgroups, void* stream);
+
 /* Message of the last failing call on this thread ("" if none). */
 const char* bp_last_error(void);
 const char* bp_status_name(bp_status status);

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
             float v = -INFINITY;
 #pragma unroll
             for (int st2 = 0; st2 < kSub; st2++)
-                v = fmaxf(v, fmaxf(fmaxf(s[h][st2][0], s[h][st2][1]), fmaxf(s[h][st2][2], s[h][st2][3])));
+                v = fmax_p(v, fmax_p(fmax_p(s[h][st2][0], s[h][st2][1]), fmax_p(s[h][st2][2], s[h][st2][3])));
             cm[h] = group_max(v) * c2;
             // Lazy rescale: the running max of a row moves only when the chunk
             // max exceeds it by more than kLazy; p then stays below 2^kLazy,

@@ -48,8 +48,13 @@ __device__ __forceinline__ LanePair xchg32(float v) {
     const uint32_t r0 = r[0], r1 = r[1];
     return {__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1)};
 }
-__device__ __forceinline__ float max_xor16(float v) { const LanePair p = xchg16(v); return fmaxf(p.a, p.b); }
-__device__ __forceinline__ float max_xor32(float v) { const LanePair p = xchg32(v); return fmaxf(p.a, p.b); }
+// IEEE-754-2019 maximum (NaN-propagating): lowers to v_maximum(3)_f32 with no
+// input canonicalization, where fmaxf (maxNum) first quiets each operand with
+// an extra v_max_f32 x, x, x when the compiler cannot prove it canonical (an
+// MFMA result or a lane exchange). Differs from fmaxf only for NaN inputs.
+__device__ __forceinline__ float fmax_p(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max_xor16(float v) { const LanePair p = xchg16(v); return fmax_p(p.a, p.b); }
+__device__ __forceinline__ float max_xor32(float v) { const LanePair p = xchg32(v); return fmax_p(p.a, p.b); }
 __device__ __forceinline__ float sum_xor16(float v) { const LanePair p = xchg16(v); return p.a + p.b; }
 __device__ __forceinline__ float sum_xor32(float v) { const LanePair p = xchg32(v); return p.a + p.b; }
 

@@ -13,7 +13,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbp_oracle.so")
+# BP_ORACLE_LIB selects another build of the same source (the sanitizer build
+# of tests/test_sanitizers.py).
+LIB_PATH = os.environ.get("BP_ORACLE_LIB") or os.path.join(HERE, "libbp_oracle.so")
 
 
 def build() -> str:

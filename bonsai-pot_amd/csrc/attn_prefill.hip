@@ -404,30 +404,33 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
         // Online softmax (m_run in log2 units). Both heads' chunk maxima and the
         // (rare) rescale come first, so that the exponentials, P^T packing and
         // the P.V / row-sum MFMAs below form one block the scheduler can interleave.
-        float cm[kHeadsPerWave];
-        bool up[kHeadsPerWave];
+        // Lazy rescale: the running max of a row moves only when the chunk max
+        // exceeds it by more than kLazy; p then stays below 2^kLazy, which f16
+        // P and the f32 accumulators hold as well as p <= 1. The test is made
+        // first on each lane's own maximum and voted over the wave; only when
+        // some lane passes it are the rows' maxima taken across their 4 lane
+        // groups (scaling by c2 > 0 commutes with max, so this is the same test
+        // and the same new max as on the row maxima).
+        float lm[kHeadsPerWave];
+        bool lane_up = false;
 #pragma unroll
         for (int h = 0; h < kHeadsPerWave; h++) {
             float v = -INFINITY;
 #pragma unroll
             for (int st2 = 0; st2 < kSub; st2++)
                 v = fmax_p(v, fmax_p(fmax_p(s[h][st2][0], s[h][st2][1]), fmax_p(s[h][st2][2], s[h][st2][3])));
-            cm[h] = group_max(v) * c2;
-            // Lazy rescale: the running max of a row moves only when the chunk
-            // max exceeds it by more than kLazy; p then stays below 2^kLazy,
-            // which f16 P and the f32 accumulators hold as well as p <= 1.
-            up[h] = cm[h] > m_run[h] + kLazy;
+            lm[h] = v * c2;
+            lane_up = lane_up || lm[h] > m_run[h] + kLazy;
         }
-        bool any_up = false;
-#pragma unroll
-        for (int h = 0; h < kHeadsPerWave; h++) any_up = any_up || up[h];
-        if (__any(any_up)) {
+        if (__any(lane_up)) {
 #pragma unroll
             for (int h = 0; h < kHeadsPerWave; h++) {
-                const float m_new = up[h] ? cm[h] : m_run[h];
+                const float cm = group_max(lm[h]);
+                const bool up = cm > m_run[h] + kLazy;
+                const float m_new = up ? cm : m_run[h];
                 // 0 from -inf, 1 if kept (also for a row whose max is still
                 // -inf, where the difference would be NaN)
-                const float alpha = up[h] ? __builtin_amdgcn_exp2f(m_run[h] - m_new) : 1.0f;
+                const float alpha = up ? __builtin_amdgcn_exp2f(m_run[h] - m_new) : 1.0f;
                 m_run[h] = m_new;
                 l_acc[h][0] *= alpha;   // only element 0 is read
 #pragma unroll

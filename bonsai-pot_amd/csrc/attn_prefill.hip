@@ -5,9 +5,10 @@
 // f16 output — computed in two passes:
 //
 // kv_dequant_kernel writes the layer's K and V for rows [0, cur of the last
-// token) as an f16 image (f16(d * q) per value): per KV head and 64-row chunk,
-// K rows and V^T (dims x key slots in the MFMA order below), 16-byte groups
-// XOR-swizzled against LDS bank conflicts, so that a chunk is one linear copy.
+// token) as an f16 image (f16(d * q) per value, plus a K residual below): per
+// KV head and 64-row chunk, K rows and V^T (dims x key slots in the MFMA order
+// below), 16-byte groups XOR-swizzled against LDS bank conflicts, so that a
+// chunk is one linear copy.
 //
 // prefill_kernel, a flash-attention over LDS tiles of that image:
 //  * Query tokens form tiles of 32; a "unit" is 16 tokens x 2 GQA heads (one
@@ -56,13 +57,13 @@ constexpr int kChunk = 64;               // cache rows per LDS chunk
 constexpr int kSub = kChunk / 16;        // 16-row S^T sub-tiles per chunk
 constexpr int kKHalves = kChunk * kHeadDim;   // K rows, 256 B each
 constexpr int kVHalves = kHeadDim * kChunk;   // V^T rows (dims), 128 B each
-constexpr int kLBytes = kChunk * kHeadDim;    // fp8 K residual rows, 128 B each
+constexpr int kLBytes = kChunk * kHeadDim;    // K residual rows, 128 B each
 constexpr int kBufHalves = kKHalves + kVHalves + kLBytes / 2;   // one staged chunk (40 KB)
-// The K residual is stored as fp8 of 2^11 (k - f16(k)); the q.k correction
-// MFMA scales its product back by 2^-11 (E8M0 exponent 127 - 11).
+// The K residual is 2^11 (k - f16(k)) in fp6 (e2m3) with one power-of-two
+// scale per 32-element block; the q.k correction MFMA applies that scale
+// times 2^-11 through its E8M0 operand.
 constexpr int kResidShift = 11;
-constexpr int kResidScaleE8M0 = 127 - kResidShift;
-constexpr int kOneE8M0 = 127;
+constexpr int kE8M0Bias = 127;
 constexpr float kLazy = 8.0f;            // lazy-rescale threshold (log2 units)
 
 struct alignas(16) U4 { uint32_t w[4]; };
@@ -71,25 +72,39 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-// c + 2^-11 (a . b) over 128 k of fp8 (e4m3) operands: the q.k correction by
-// the K residual. Lane l holds 32 k-values of row / column l % 16 in each
-// operand, the same k set for A and B, so the product pairs them whatever
-// order the hardware walks k in.
-__device__ __forceinline__ f32x4 mfma_resid(i32x8 a, i32x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, kResidScaleE8M0, 0, kOneE8M0);
+// c + (a . b) over 128 k of fp6 (e2m3) operands, each lane's 32 values
+// scaled by 2^(sa - 127) (A) and 2^(sb - 127) (B): the q.k correction by the
+// K residual. Lane l holds 32 k-values of row / column l % 16 in each
+// operand, packed in the same element order for A and B (both by
+// pack32_fp6), so the product pairs them whatever order the hardware walks k
+// in. Elements 6, 7 of a and b are unused (fp6 operands are 6 registers).
+__device__ __forceinline__ f32x4 mfma_resid(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 2, 2, 0, sa, 0, sb);
 }
-// Two floats -> two e4m3 bytes (round to nearest even) in half kHi of `old`.
-// Inputs are clamped to the format's +-448 first (out-of-range values would
-// otherwise convert to NaN).
-template <bool kHi>
-__device__ __forceinline__ int pack_fp8(float a, float b, int old) {
-    a = fminf(fmaxf(a, -448.0f), 448.0f);
-    b = fminf(fmaxf(b, -448.0f), 448.0f);
-    return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, old, kHi);
+// Exponent e of the power-of-two block scale for fp6 e2m3 (largest finite
+// 7.5): the smallest e with amax / 2^e <= 7.5, at least e_min, 0 for an
+// all-zero block. From the bits of amax: amax = 1.f * 2^E, amax / 2^(E-2) =
+// 4 * 1.f lies in [4, 8) and exceeds 7.5 exactly when f > 0.875.
+__device__ __forceinline__ int fp6_scale_exp(float amax, int e_min) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, amax);
+    if ((b & 0x7F800000u) == 0) return amax > 0.0f ? e_min : 0;   // zero or subnormal
+    int e = static_cast<int>((b >> 23) & 0xFFu) - 127 - 2;
+    if ((b & 0x007FFFFFu) > 0x00700000u) ++e;
+    return e < e_min ? e_min : e;
 }
-// Four floats -> four e4m3 bytes (little-endian order).
-__device__ __forceinline__ int pack4_fp8(float a, float b, float c, float d) {
-    return pack_fp8<true>(c, d, pack_fp8<false>(a, b, 0));
+// 32 floats / 2^e -> 32 fp6 e2m3 values (round to nearest even, saturating at
+// +-7.5) packed 6 bits each into 6 words. The hardware conversion takes two
+// 16-value halves and interleaves them: element 2j is v[j], 2j + 1 is v[16 + j].
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x6 __attribute__((ext_vector_type(6)));
+__device__ __forceinline__ i32x6 pack32_fp6(const float (&v)[32], int e) {
+    f32x16 lo, hi;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        lo[i] = v[i];
+        hi[i] = v[16 + i];
+    }
+    return __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23));
 }
 
 // Position of chunk row `key` (0..63) along the MFMA k axis of the PV step:
@@ -130,9 +145,11 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 // Dequantization pass: one 256-thread workgroup per (64-row chunk, KV head)
-// writes the chunk's K rows (f16 and fp8 residual) and its V^T (dims x slots,
+// writes the chunk's K rows (f16 and fp6 residual) and its V^T (dims x slots,
 // keys in v_slot order) to the image, zeros past n_rows. Each value is the
-// reference's f32 d * q; K keeps f16(k) plus e4m3(2^11 (k - f16(k))), V
+// reference's f32 d * q; K keeps f16(k) plus 2^11 (k - f16(k)) in fp6 e2m3
+// with one power-of-two scale per 32-element block (the residual of a block:
+// 6 words of fp6, its E8M0 scale exponent less 11 in word 6, word 7 zero), V
 // keeps f16(v).
 //  K: thread t -> row t >> 2, Q8_0 block t & 3 (32 dims: 64 + 32 bytes out).
 //  V: thread t -> rows 4 (t >> 4) .. +3, dims 8 (t & 15) .. +7; each dim's 4
@@ -164,26 +181,33 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
         if (row > last) vd[i] = 0.0f;
     }
     if (krow > last) kd = 0.0f;
-    // ---- K rows: f16 value and fp8 residual of k = d * q (f32, as the
+    // ---- K rows: f16 value and fp6 residual of k = d * q (f32, as the
     // reference dequantizes) ----
     {
         uint32_t w[16];
-        int lo[8];
+        float r[32];
+        float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const uint32_t x = i < 4 ? kq0.w[i] : kq1.w[i - 4];
-            float k[4], r[4];
+            float k[4];
             _Float16 h[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 k[e] = kd * static_cast<float>(static_cast<int8_t>(x >> (8 * e)));
                 h[e] = static_cast<_Float16>(k[e]);
-                r[e] = (k[e] - static_cast<float>(h[e])) * static_cast<float>(1 << kResidShift);
+                r[4 * i + e] = (k[e] - static_cast<float>(h[e])) * static_cast<float>(1 << kResidShift);
+                amax = fmaxf(amax, fabsf(r[4 * i + e]));
             }
             w[2 * i] = __builtin_bit_cast(uint32_t, f16x2{h[0], h[1]});
             w[2 * i + 1] = __builtin_bit_cast(uint32_t, f16x2{h[2], h[3]});
-            lo[i] = pack4_fp8(r[0], r[1], r[2], r[3]);
         }
+        // block scale 2^e, applied by the MFMA as E8M0 e + 127 - 11 (>= 0)
+        const int e = fp6_scale_exp(amax, kResidShift - kE8M0Bias);
+        const i32x6 p6 = pack32_fp6(r, e);
+        const uint32_t lo[8] = {static_cast<uint32_t>(p6[0]), static_cast<uint32_t>(p6[1]), static_cast<uint32_t>(p6[2]),
+                                static_cast<uint32_t>(p6[3]), static_cast<uint32_t>(p6[4]), static_cast<uint32_t>(p6[5]),
+                                static_cast<uint32_t>(e + kE8M0Bias - kResidShift), 0u};
         uint16_t* kdst = a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves;
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -191,9 +215,7 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
         uint8_t* ldst = a.kl8 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kLBytes;
 #pragma unroll
         for (int i = 0; i < 2; i++)
-            *reinterpret_cast<U4*>(ldst + l_addr(kr, 2 * kb + i)) =
-                U4{{static_cast<uint32_t>(lo[4 * i]), static_cast<uint32_t>(lo[4 * i + 1]),
-                    static_cast<uint32_t>(lo[4 * i + 2]), static_cast<uint32_t>(lo[4 * i + 3])}};
+            *reinterpret_cast<U4*>(ldst + l_addr(kr, 2 * kb + i)) = U4{{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]}};
     }
     // ---- V^T through LDS: f16(d * q) ----
     {
@@ -262,7 +284,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     uint32_t wtok0 = 0, my_tok = 0, my_kend = 0, wave_kend = 0;
     bool unit_live = false;
     f16x8 qb[kHeadsPerWave][4];
-    i32x8 q8[kHeadsPerWave];   // q of token my_tok, dims 32 lg .. +32, as e4m3 (residual MFMA)
+    i32x8 q6[kHeadsPerWave];   // q of token my_tok, dims 32 lg .. +32, as fp6 (residual MFMA)
+    int q6s[kHeadsPerWave];    // its E8M0 block scale
     f32x4 o[kHeadsPerWave][8];
     float m_run[kHeadsPerWave], l_run[kHeadsPerWave];
     f32x4 l_acc[kHeadsPerWave];   // row sums of P (every element holds the token's sum)
@@ -291,14 +314,21 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                     for (int i = 0; i < 4; i++) raw[i] = *reinterpret_cast<const U4*>(qp + 8 * i);
                 }
+                float qf[32];
+                float amax = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const f16x8 v = __builtin_bit_cast(f16x8, raw[i]);
-                    q8[h][2 * i] = pack4_fp8(static_cast<float>(v[0]), static_cast<float>(v[1]),
-                                             static_cast<float>(v[2]), static_cast<float>(v[3]));
-                    q8[h][2 * i + 1] = pack4_fp8(static_cast<float>(v[4]), static_cast<float>(v[5]),
-                                                 static_cast<float>(v[6]), static_cast<float>(v[7]));
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        qf[8 * i + j] = static_cast<float>(v[j]);
+                        amax = fmaxf(amax, fabsf(qf[8 * i + j]));
+                    }
                 }
+                const int e = fp6_scale_exp(amax, -126);
+                const i32x6 p6 = pack32_fp6(qf, e);
+                q6[h] = i32x8{p6[0], p6[1], p6[2], p6[3], p6[4], p6[5], 0, 0};
+                q6s[h] = e + kE8M0Bias;
             }
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -375,18 +405,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int h = 0; h < kHeadsPerWave; h++) s[h][st2] = mfma16(ka[st2], qb[h][kk], s[h][st2]);
         }
-        // Residual correction: s += 2^-11 (K residual . q) on the fp8 matrix
-        // path, one 128-deep MFMA per sub-tile and head.
+        // Residual correction: s += K residual . q on the fp6 matrix path, one
+        // 128-deep MFMA per sub-tile and head; the lane's 32 bytes are its 32
+        // residual values (6 words) and their E8M0 scale (word 6).
 #pragma unroll
         for (int st2 = 0; st2 < kSub; st2++) {
             const int row = 16 * st2 + lr;
             const U4 r0 = *reinterpret_cast<const U4*>(lb + l_addr(row, 2 * lg));
             const U4 r1 = *reinterpret_cast<const U4*>(lb + l_addr(row, 2 * lg + 1));
             const i32x8 ra = {static_cast<int>(r0.w[0]), static_cast<int>(r0.w[1]), static_cast<int>(r0.w[2]),
-                              static_cast<int>(r0.w[3]), static_cast<int>(r1.w[0]), static_cast<int>(r1.w[1]),
-                              static_cast<int>(r1.w[2]), static_cast<int>(r1.w[3])};
+                              static_cast<int>(r0.w[3]), static_cast<int>(r1.w[0]), static_cast<int>(r1.w[1]), 0, 0};
+            const int sa = static_cast<int>(r1.w[2]);
 #pragma unroll
-            for (int h = 0; h < kHeadsPerWave; h++) s[h][st2] = mfma_resid(ra, q8[h], s[h][st2]);
+            for (int h = 0; h < kHeadsPerWave; h++) s[h][st2] = mfma_resid(ra, q6[h], s[h][st2], sa, q6s[h]);
         }
         issue();
         // Mask (only chunks that reach past the unit's earliest visible row);

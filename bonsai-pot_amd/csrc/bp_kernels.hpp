@@ -93,9 +93,10 @@ struct PrefillArgs {
     // rows [0, n_rows) (zeros up to the next 64-row chunk), per KV head g:
     // K   at k16  + (g * ws_chunks + c) * 64 * 128: f16 rows of chunk c, row-major;
     // V^T at vt16 + (g * ws_chunks + c) * 128 * 64: f16 dims of chunk c, slot-major;
-    // K residual at kl8 + (g * ws_chunks + c) * 64 * 128 bytes: per row, the
-    //   fp8 (e4m3) value of 2^11 * (k - f16(k)), so that f16 + residual carry
-    //   the f32 key to about 15 bits.
+    // K residual at kl8 + (g * ws_chunks + c) * 64 * 128 bytes: per row and
+    //   32-element block, 2^11 * (k - f16(k)) as fp6 (e2m3) with a power-of-two
+    //   block scale (32 bytes: 6 words of fp6, the scale in word 6), so that
+    //   f16 + residual carry the f32 key to about 15 bits.
     uint16_t* k16;
     uint16_t* vt16;
     uint8_t* kl8;
@@ -103,7 +104,7 @@ struct PrefillArgs {
     uint32_t n_rows;          // rows the queries attend: cur of the last token
 };
 // Bytes of the K/V image for max_seq rows (one layer): f16 K, f16 V^T and
-// the fp8 K residual, 640 bytes per (row, KV head).
+// the K residual, 640 bytes per (row, KV head).
 inline uint64_t prefill_image_bytes(uint32_t n_kv_head, uint32_t max_seq) {
     return 5ull * n_kv_head * ((max_seq + 63) / 64) * 64 * 128;
 }

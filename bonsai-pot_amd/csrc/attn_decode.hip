@@ -258,7 +258,8 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     float bsum = 0.0f;   // column (hq, bq) sum of W, for the 1152 bias of V
     const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
-    auto consume = [&](const Batch& B, uint32_t b, bool tail) {
+    // Scores of one batch (head hq, rows 4 lg + j), -inf past row_end.
+    auto scores = [&](const Batch& B, uint32_t b, bool tail, float (&s)[4]) {
         // q.k on the matrix core: 4 MFMAs over the 32 bytes of block lg of row lr.
         f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -270,7 +271,6 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
             d = mfma32(__builtin_bit_cast(f16x8, kw), qop[i], d);
         }
         // s(row 4 lg + j, head hq) = sum over the 4 blocks (the lane quad) of d_b * (D - bias).
-        float s[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             float v = B.kd[j] * (d[j] - qb);
@@ -283,8 +283,11 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
 #pragma unroll
             for (int j = 0; j < 4; j++) s[j] = r0 + j < row_end ? s[j] : -INFINITY;
         }
-        float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        bm = max_xor32(max_xor16(bm));
+    };
+    // Running max of head hq over the rows seen so far (exact), with the
+    // rescale of O and the sums when it moves.
+    auto update_max = [&](float bl) {
+        const float bm = max_xor32(max_xor16(bl));
         const float m_new = fmaxf(m_run, bm);
         if (__builtin_amdgcn_ballot_w64(m_new != m_run) != 0) {
             const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);   // 0 on the first batch
@@ -295,6 +298,9 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
             for (int i = 0; i < 8; i++) oacc[i] *= ao;
             m_run = m_new;
         }
+    };
+    // p = exp2 of the scores and O^T += W^T V for one batch.
+    auto pv = [&](const Batch& B, const float (&s)[4]) {
         const float mc = m_run * c2;
         float w[4];
 #pragma unroll
@@ -342,9 +348,31 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
         }
     };
 
+    auto consume = [&](const Batch& B, uint32_t b, bool tail) {
+        float s[4];
+        scores(B, b, tail, s);
+        update_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+        pv(B, s);
+    };
+    // Two batches as one: both batches' scores first (independent MFMA and
+    // VALU chains), one max update, then both P.V steps.
+    auto consume2 = [&](const Batch& B0, uint32_t b0, const Batch& B1, uint32_t b1, bool tail) {
+        float s0[4], s1[4];
+        scores(B0, b0, false, s0);
+        scores(B1, b1, tail, s1);
+        update_max(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
+        pv(B0, s0);
+        pv(B1, s1);
+    };
+
     // Loads are unconditional (an index past the end re-reads the last batch,
     // an L2 hit) so that each wait leaves the next batch in flight.
-    if (n_batches > 0) {
+    if (n_batches == 2) {
+        // the two batches are already both in flight: consume them together
+        load(Bb, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        consume2(A, 0, Bb, 1, true);
+    } else if (n_batches > 0) {
         uint32_t b = 0;
         while (true) {
             load(Bb, min(b + 1, last_b));

@@ -293,7 +293,13 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
             const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c2);   // 0 on the first batch
             lsum *= alpha;
             bsum *= alpha;
-            const float ao = __shfl(alpha, 4 * lg);   // head lg
+            // alpha of head lg: every lane of head h's quads holds it; lane
+            // 20 h (lr = 4 h, row h) is read into a scalar register per head
+            const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 0));
+            const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 20));
+            const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 40));
+            const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 60));
+            const float ao = lg == 0 ? a0 : lg == 1 ? a1 : lg == 2 ? a2 : a3;   // head lg
 #pragma unroll
             for (int i = 0; i < 8; i++) oacc[i] *= ao;
             m_run = m_new;

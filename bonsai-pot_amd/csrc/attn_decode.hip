@@ -125,15 +125,23 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     const int hq = lr >> 2, bq = lr & 3;   // the (head, block) column of this lane
     // Wave w streams KV head kH hg + (w % kH), row set w / kH (see SplitShape).
     // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
-    // linear id, so ids are laid out as [split / 8][hg][split % 8] — the head
-    // groups of one split share an XCD and hence its L2 copy of the rows' FP32
-    // scale lines (one 128-byte line holds the scales of all heads of a row).
+    // linear id (x fastest, then y, then z), so the grid is (split % 8, hg,
+    // split / 8) — the head groups of one split share an XCD and hence its L2
+    // copy of the rows' FP32 scale lines (one 128-byte line holds the scales of
+    // all heads of a row). Three grid dimensions instead of a 1-D id keep two
+    // integer divisions out of the kernel's start.
     const int hw = wave % kH, rs = wave / kH;
-    const uint32_t ngr = gridDim.x / ((a.n_splits + 7) / 8 * 8);
-    const uint32_t within = blockIdx.x % (8 * ngr);
-    const uint32_t hg = within / 8;
+    const uint32_t hg = blockIdx.y;
     const uint32_t g = hg * kH + hw;
-    const uint32_t split = blockIdx.x / (8 * ngr) * 8 + within % 8;
+    const uint32_t split = blockIdx.z * 8 + blockIdx.x;
+    // All arguments the first loads need are requested in one batch of scalar
+    // loads (otherwise the idle-workgroup test below waits for n_splits first
+    // and the rest is fetched in a second round trip).
+    asm volatile("" ::"s"(a.n_rows), "s"(a.split_len), "s"(a.kv_dim), "s"(a.k.qs), "s"(a.k.d), "s"(a.v.qs),
+                 "s"(a.v.d), "s"(a.q));
+    if constexpr (kFused)
+        asm volatile("" ::"s"(a.w_norms), "s"(a.rope_cs), "s"(a.pos), "s"(a.w_q_off), "s"(a.w_k_off),
+                     "s"(a.k_cur), "s"(a.v_cur));
     if (split >= a.n_splits) return;
     const uint32_t row0 = min(split * a.split_len, a.n_rows);
     const uint32_t row_end = min(row0 + a.split_len, a.n_rows);
@@ -566,12 +574,12 @@ uint32_t decode_partial_stride() { return kPartStride; }
 
 template <bool kFused>
 static void launch_split(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    const uint32_t rows8 = (a.n_splits + 7) / 8 * 8;
+    const uint32_t z = (a.n_splits + 7) / 8;
     if (a.heads_per_wg == 4)
-        hipLaunchKernelGGL((decode_split_kernel<kFused, 4>), dim3(rows8 * (n_kv_head / 4)),
+        hipLaunchKernelGGL((decode_split_kernel<kFused, 4>), dim3(8, n_kv_head / 4, z),
                            dim3(SplitShape<4>::kThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((decode_split_kernel<kFused, 1>), dim3(rows8 * n_kv_head),
+        hipLaunchKernelGGL((decode_split_kernel<kFused, 1>), dim3(8, n_kv_head, z),
                            dim3(SplitShape<1>::kThreads), 0, s, a);
 }
 

@@ -18,8 +18,12 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 SOURCES = ["bp_api.cpp", "norm_rope_writeback.hip", "attn_decode.hip", "attn_prefill.hip", "matvec_q1_0.hip", "matvec_q1_0_mfma.hip", "matmul_q1_0_q8_0.hip", "topk_reduce.hip", "read_floor.hip"]
 # Per-source additions: the matmul's MFMA results go straight to VGPRs (the
 # default AGPR form costs one v_accvgpr_read per result element in its f32
-# epilogue).
-EXTRA_FLAGS = {"matmul_q1_0_q8_0.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# epilogue); the decode kernels' leading scalar arguments (up to 14 dwords)
+# are preloaded into SGPRs at wave launch instead of fetched by the first
+# scalar loads (a kernel built this way also runs where the command processor
+# does not preload: its entry code then loads them itself).
+EXTRA_FLAGS = {"matmul_q1_0_q8_0.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "attn_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 FLAGS = [
     "-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-ffp-contract=off", "-Wall", "-Wno-unused-function",

@@ -460,13 +460,15 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
 // One wave per (query head, 32-dim chunk); kLoads = 8 (up to 64 splits) or
 // 16 (up to 128) partial loads per lane.
 template <bool kFused, int kLoads>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64) void decode_merge_kernel(
+    float* partials_, uint32_t n_splits_, uint32_t kv_dim_, const uint16_t* q_norm_, const float* kd_row_,
+    const int8_t* kq_row_, const float* vd_row_, const int8_t* vq_row_, DecodeArgs a) {
     const int lane = threadIdx.x;
     const uint32_t h = blockIdx.x >> 2, c = blockIdx.x & 3;
     const uint32_t g = h / kGroup;
-    const uint32_t ns = a.n_splits;
-    const float* ph = part_o(a.partials, h, ns, 0);
-    const float* pml = part_ml(a.partials, a.kv_dim / kHeadDim * kGroup, h, ns, 0);
+    const uint32_t ns = n_splits_;
+    const float* ph = part_o(partials_, h, ns, 0);
+    const float* pml = part_ml(partials_, kv_dim_ / kHeadDim * kGroup, h, ns, 0);
     const float c2 = a.scale * kLog2e;
 
     // O chunk loads: lane -> splits (lane >> 3) + 8i, dims 32c + 4 (lane & 7) .. +3.
@@ -492,13 +494,11 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
     float vd_new = 0.0f;
     uint32_t vq_new = 0;
     if constexpr (kFused) {
-        const uint64_t row = a.pos;
-        const uint32_t nb_row = a.kv_dim / kBlock;
-        const uint16_t* qn = a.q_norm + static_cast<uint64_t>(h) * kHeadDim;
-        const float* kd = a.k.d + row * nb_row + g * (kHeadDim / kBlock);
-        const int8_t* kq = a.k.qs + row * a.kv_dim + g * kHeadDim;
-        vd_new = a.v.d[row * nb_row + g * (kHeadDim / kBlock) + (d0 >> 5)];
-        vq_new = *reinterpret_cast<const uint32_t*>(a.v.qs + row * a.kv_dim + g * kHeadDim + d0);
+        const uint16_t* qn = q_norm_ + static_cast<uint64_t>(h) * kHeadDim;
+        const float* kd = kd_row_ + g * (kHeadDim / kBlock);
+        const int8_t* kq = kq_row_ + g * kHeadDim;
+        vd_new = vd_row_[g * (kHeadDim / kBlock) + (d0 >> 5)];
+        vq_new = *reinterpret_cast<const uint32_t*>(vq_row_ + g * kHeadDim + d0);
         const uint16_t qa = qn[lane], qb = qn[lane + 64];
         const float q0 = h2f(qa), q1 = h2f(qb);
         const float k0 = kd[lane >> 5] * static_cast<float>(kq[lane]);
@@ -583,12 +583,24 @@ static void launch_split(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s)
                            dim3(SplitShape<1>::kThreads), 0, s, a);
 }
 
+// The arguments of the merge pass's first loads go first and as scalars, so
+// that they are preloaded into SGPRs at wave launch (this file is compiled with
+// kernarg preloading) instead of fetched by the wave's first scalar loads; the
+// fused step's row `pos` is passed as row pointers for the same reason.
 template <bool kFused>
 static void launch_merge(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {
+    const uint64_t row = a.pos;
+    const uint32_t nb_row = a.kv_dim / kBlock;
+    const float* kd_row = kFused ? a.k.d + row * nb_row : nullptr;
+    const int8_t* kq_row = kFused ? a.k.qs + row * a.kv_dim : nullptr;
+    const float* vd_row = kFused ? a.v.d + row * nb_row : nullptr;
+    const int8_t* vq_row = kFused ? a.v.qs + row * a.kv_dim : nullptr;
     if (a.n_splits > 64)
-        hipLaunchKernelGGL((decode_merge_kernel<kFused, 16>), dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
+        hipLaunchKernelGGL((decode_merge_kernel<kFused, 16>), dim3(n_kv_head * kGroup * 4), dim3(64), 0, s,
+                           a.partials, a.n_splits, a.kv_dim, a.q_norm, kd_row, kq_row, vd_row, vq_row, a);
     else
-        hipLaunchKernelGGL((decode_merge_kernel<kFused, 8>), dim3(n_kv_head * kGroup * 4), dim3(64), 0, s, a);
+        hipLaunchKernelGGL((decode_merge_kernel<kFused, 8>), dim3(n_kv_head * kGroup * 4), dim3(64), 0, s,
+                           a.partials, a.n_splits, a.kv_dim, a.q_norm, kd_row, kq_row, vd_row, vq_row, a);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s) {

@@ -178,8 +178,10 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     // ---- query-side loads first (unconditional): waiting for them below then
     // leaves the first batch of rows in flight (loads retire in order). -----------
     const uint16_t* cs = a.rope_cs + static_cast<uint64_t>(a.pos) * kHeadDim + 2 * lane;
-    float qx[kQPerWave][2] = {}, w0 = 0.f, w1 = 0.f, c0 = 0.f, s0 = 0.f;
-    float x0 = 0.f, x1 = 0.f, kw0 = 0.f, kw1 = 0.f;
+    // (kept as raw f16 bits until the first batch is requested: a conversion
+    // here would wait for these loads before the batch's loads are issued)
+    uint16_t qxr[kQPerWave][2] = {}, w0r = 0, w1r = 0, x0r = 0, x1r = 0, kw0r = 0, kw1r = 0;
+    uint32_t csr = 0;
     Q16 qraw[4];   // q of head hq, dims 32 lg + 8 i .. +8
     // Fused step: wave w normalizes the workgroup's query heads kQPerWave w ..,
     // and waves w < 2 kH write row `pos` of KV head kH hg + (w % kH): K for
@@ -190,18 +192,17 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
         const uint16_t* qr = a.q + static_cast<uint64_t>(qh0) * kHeadDim;
 #pragma unroll
         for (int i = 0; i < kQPerWave; i++) {
-            qx[i][0] = h2f(qr[i * kHeadDim + lane]);
-            qx[i][1] = h2f(qr[i * kHeadDim + lane + 64]);
+            qxr[i][0] = qr[i * kHeadDim + lane];
+            qxr[i][1] = qr[i * kHeadDim + lane + 64];
         }
-        w0 = h2f(a.w_norms[a.w_q_off + lane]);
-        w1 = h2f(a.w_norms[a.w_q_off + lane + 64]);
-        c0 = h2f(cs[0]);
-        s0 = h2f(cs[1]);
+        w0r = a.w_norms[a.w_q_off + lane];
+        w1r = a.w_norms[a.w_q_off + lane + 64];
+        csr = *reinterpret_cast<const uint32_t*>(cs);
         const uint16_t* src = (wave < kH ? a.k_cur : a.v_cur) + g_wb * kHeadDim;   // writeback input
-        x0 = h2f(src[lane]);
-        x1 = h2f(src[lane + 64]);
-        kw0 = h2f(a.w_norms[a.w_k_off + lane]);
-        kw1 = h2f(a.w_norms[a.w_k_off + lane + 64]);
+        x0r = src[lane];
+        x1r = src[lane + 64];
+        kw0r = a.w_norms[a.w_k_off + lane];
+        kw1r = a.w_norms[a.w_k_off + lane + 64];
     } else {
         const uint16_t* qp = a.q + (static_cast<uint64_t>(g) * kGroup + hq) * kHeadDim + 32 * lg;
 #pragma unroll
@@ -214,6 +215,13 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (kFused) {
+        float qx[kQPerWave][2];
+#pragma unroll
+        for (int i = 0; i < kQPerWave; i++) { qx[i][0] = h2f(qxr[i][0]); qx[i][1] = h2f(qxr[i][1]); }
+        const float w0 = h2f(w0r), w1 = h2f(w1r), c0 = h2f(static_cast<uint16_t>(csr)),
+                    s0 = h2f(static_cast<uint16_t>(csr >> 16));
+        float x0 = h2f(x0r), x1 = h2f(x1r);
+        const float kw0 = h2f(kw0r), kw1 = h2f(kw1r);
         // q_norm_rope (q_norm_rope_fused.wgsl:38-96), into LDS.
         uint16_t* qn = &qn_sh[0][0][0] + kQPerWave * wave * kHeadDim;
         uint16_t* qg = a.q_norm + static_cast<uint64_t>(qh0) * kHeadDim;

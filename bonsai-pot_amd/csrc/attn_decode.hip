@@ -92,9 +92,13 @@ __device__ __forceinline__ f32x4 mfma32(f16x8 a, f16x8 b, f32x4 c) {
 __device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
-// Pick element i (0..3) of a 4-vector with a non-uniform i.
+// Pick element i (0..3) of a 4-vector with a non-uniform i: three selects on
+// the bits of i (a chain of ternaries on i compiles to branches).
 __device__ __forceinline__ float pick4(f32x4 v, int i) {
-    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+    const bool b0 = (i & 1) != 0, b1 = (i & 2) != 0;
+    const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+    const float lo = b0 ? v1 : v0, hi = b0 ? v3 : v2;
+    return b1 ? hi : lo;
 }
 
 template <int kCtrl>

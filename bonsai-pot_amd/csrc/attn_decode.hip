@@ -319,7 +319,7 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
             const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 20));
             const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 40));
             const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 60));
-            const float ao = lg == 0 ? a0 : lg == 1 ? a1 : lg == 2 ? a2 : a3;   // head lg
+            const float ao = pick4(f32x4{a0, a1, a2, a3}, lg);   // head lg
 #pragma unroll
             for (int i = 0; i < 8; i++) oacc[i] *= ao;
             m_run = m_new;

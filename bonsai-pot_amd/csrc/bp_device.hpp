@@ -18,16 +18,6 @@ __device__ __forceinline__ uint16_t f2h(float x) {  // v_cvt_f16_f32: round to n
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 
 // Lane exchanges across 16- and 32-lane rows without LDS: v_permlane16_swap /
 // v_permlane32_swap of a register with itself leave, in every lane, the pair
@@ -76,6 +66,27 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
 template <int S>
 __device__ __forceinline__ float lane_xor(float v) {
     return __builtin_bit_cast(float, lane_xor<S>(__builtin_bit_cast(uint32_t, v)));
+}
+
+// Butterfly reductions over the wave (partners lane ^ 32, ^ 16, .., ^ 1, so
+// every lane ends with the same value): row exchanges by v_permlane32/16_swap
+// and DPP lane moves, no LDS round trip per step.
+__device__ __forceinline__ float wave_max(float v) {
+    LanePair p = xchg32(v);
+    v = fmaxf(p.a, p.b);
+    p = xchg16(v);
+    v = fmaxf(p.a, p.b);
+    v = fmaxf(v, lane_xor<8>(v));
+    v = fmaxf(v, lane_xor<4>(v));
+    v = fmaxf(v, lane_xor<2>(v));
+    return fmaxf(v, lane_xor<1>(v));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = sum_xor16(sum_xor32(v));
+    v += lane_xor<8>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<2>(v);
+    return v + lane_xor<1>(v);
 }
 // Value of lane 4 (lane / 4) + K (a quad broadcast).
 template <int K>

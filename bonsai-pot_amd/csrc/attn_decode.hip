@@ -491,13 +491,27 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
         const uint32_t s = min(static_cast<uint32_t>((lane >> 3) + 8 * i), ns - 1);
         ov[i] = *reinterpret_cast<const float4*>(ph + static_cast<uint64_t>(s) * kHeadDim + 32 * c + 4 * f4);
     }
-    // (m, l) of splits lane and lane + 64.
-    const uint32_t ls0 = min(static_cast<uint32_t>(lane), ns - 1), ls1 = min(static_cast<uint32_t>(lane) + 64u, ns - 1);
-    const float2 ml0 = *reinterpret_cast<const float2*>(pml + 2 * ls0);
-    float2 ml1 = make_float2(-INFINITY, 0.0f);
-    if constexpr (kLoads > 8) ml1 = *reinterpret_cast<const float2*>(pml + 2 * ls1);
-    const float m_s0 = static_cast<uint32_t>(lane) < ns ? ml0.x : -INFINITY;
-    const float m_s1 = static_cast<uint32_t>(lane) + 64u < ns ? ml1.x : -INFINITY;
+    // (m, l): with kLoads = 8 (up to 64 splits) of the same splits as this
+    // lane's O loads, (lane >> 3) + 8 i, so that the weights are computed
+    // in-lane; with 16, of splits lane and lane + 64 (two loads; the weights
+    // are then exchanged between lanes, which measured faster there).
+    constexpr bool kInLane = kLoads <= 8;
+    float2 mlv[kLoads];
+    float m_s0 = -INFINITY, m_s1 = -INFINITY;
+    float2 ml0 = make_float2(-INFINITY, 0.0f), ml1 = make_float2(-INFINITY, 0.0f);
+    if constexpr (kInLane) {
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) {
+            const uint32_t s = min(static_cast<uint32_t>((lane >> 3) + 8 * i), ns - 1);
+            mlv[i] = *reinterpret_cast<const float2*>(pml + 2 * s);
+        }
+    } else {
+        const uint32_t ls0 = min(static_cast<uint32_t>(lane), ns - 1), ls1 = min(static_cast<uint32_t>(lane) + 64u, ns - 1);
+        ml0 = *reinterpret_cast<const float2*>(pml + 2 * ls0);
+        ml1 = *reinterpret_cast<const float2*>(pml + 2 * ls1);
+        m_s0 = static_cast<uint32_t>(lane) < ns ? ml0.x : -INFINITY;
+        m_s1 = static_cast<uint32_t>(lane) + 64u < ns ? ml1.x : -INFINITY;
+    }
 
     float s_new = -INFINITY;   // log2-domain score of the new row (fused step)
     // Row `pos` of V for dims d0 .. d0 + 3 (lanes 0-7 use it), loaded up front with
@@ -520,20 +534,44 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
         const uint16_t qv = static_cast<uint16_t>(__shfl(static_cast<int>(c < 2 ? qa : qb), static_cast<int>((32 * c + lane) & 63)));
         if (lane < 32) a.q_act[h * kHeadDim + 32 * c + lane] = qv;
     }
-    const float M = fmaxf(wave_max(fmaxf(m_s0, m_s1)), s_new);
-    const float w0 = m_s0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s0 - M);   // 0 for splits >= ns
-    const float w1 = m_s1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s1 - M);
-    const float w_new = kFused ? __builtin_amdgcn_exp2f(s_new - M) : 0.0f;
-    const float L = wave_sum(w0 * (m_s0 == -INFINITY ? 0.0f : ml0.y) + w1 * (m_s1 == -INFINITY ? 0.0f : ml1.y)) + w_new;
-
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float M, L, w_new;
+    if constexpr (kInLane) {
+        float mloc = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-        const float wi = __shfl(i < 8 ? w0 : w1, (lane >> 3) + 8 * (i & 7));
-        acc.x = __builtin_fmaf(wi, ov[i].x, acc.x);
-        acc.y = __builtin_fmaf(wi, ov[i].y, acc.y);
-        acc.z = __builtin_fmaf(wi, ov[i].z, acc.z);
-        acc.w = __builtin_fmaf(wi, ov[i].w, acc.w);
+        for (int i = 0; i < kLoads; i++) {
+            if (static_cast<uint32_t>((lane >> 3) + 8 * i) >= ns) mlv[i].x = -INFINITY;   // clamped re-reads
+            mloc = fmaxf(mloc, mlv[i].x);
+        }
+        M = fmaxf(wave_max(mloc), s_new);
+        w_new = kFused ? __builtin_amdgcn_exp2f(s_new - M) : 0.0f;
+        float lloc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) {
+            // 0 for splits >= ns and for splits without rows (m = -inf)
+            const float wi = mlv[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mlv[i].x - M);
+            lloc = __builtin_fmaf(wi, mlv[i].x == -INFINITY ? 0.0f : mlv[i].y, lloc);
+            acc.x = __builtin_fmaf(wi, ov[i].x, acc.x);
+            acc.y = __builtin_fmaf(wi, ov[i].y, acc.y);
+            acc.z = __builtin_fmaf(wi, ov[i].z, acc.z);
+            acc.w = __builtin_fmaf(wi, ov[i].w, acc.w);
+        }
+        // the 8 lane groups (lane >> 3) hold disjoint split sets: sum over them
+        L = sum_slots(lloc) + w_new;
+    } else {
+        M = fmaxf(wave_max(fmaxf(m_s0, m_s1)), s_new);
+        const float w0 = m_s0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s0 - M);   // 0 for splits >= ns
+        const float w1 = m_s1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_s1 - M);
+        w_new = kFused ? __builtin_amdgcn_exp2f(s_new - M) : 0.0f;
+        L = wave_sum(w0 * (m_s0 == -INFINITY ? 0.0f : ml0.y) + w1 * (m_s1 == -INFINITY ? 0.0f : ml1.y)) + w_new;
+#pragma unroll
+        for (int i = 0; i < kLoads; i++) {
+            const float wi = __shfl(i < 8 ? w0 : w1, (lane >> 3) + 8 * (i & 7));
+            acc.x = __builtin_fmaf(wi, ov[i].x, acc.x);
+            acc.y = __builtin_fmaf(wi, ov[i].y, acc.y);
+            acc.z = __builtin_fmaf(wi, ov[i].z, acc.z);
+            acc.w = __builtin_fmaf(wi, ov[i].w, acc.w);
+        }
     }
     acc.x = sum_slots(acc.x);
     acc.y = sum_slots(acc.y);

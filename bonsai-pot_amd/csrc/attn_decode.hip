@@ -119,7 +119,7 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     __shared__ __attribute__((aligned(16))) uint16_t qn_sh[kH][kGroup][kHeadDim];
 
     const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);   // uniform: scalar registers
     // Lane roles, all from (lr, lg) = (lane & 15, lane >> 4):
     //  q.k   A = K rows (m = row lr), B = q masked per block (n = lr = 4 h + b),
     //        so D lane holds the block-b partial dot of head h for rows 4 lg + j;
@@ -162,18 +162,22 @@ __global__ __launch_bounds__(SplitShape<kH>::kThreads, SplitShape<kH>::kWgPerCu)
     const uint32_t vcol = g * kHeadDim + 8 * lr;           // p.v: dims 8 lr .. +8
     const uint32_t dcol = g * (kHeadDim / kBlock) + bq;    // scale of block bq
     auto load = [&](Batch& B, uint32_t b) {
+        // row r0 + y, clamped to row_last, as base + min(y, lim) with a uniform
+        // base and limit: the per-lane products are 24-bit (y < 16)
         const uint32_t r0 = row0 + 16u * (kRowSets * b + rs);
-        const uint32_t rk = min(r0 + lr, row_last);
-        B.kq[0] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol));
-        B.kq[1] = *reinterpret_cast<const Q16*>(a.k.qs + (rk * kv_dim + kcol + 16));
+        const uint32_t base = min(r0, row_last), lim = row_last - base;
+        const uint32_t qs_base = base * kv_dim, d_base = base * nb_row;
+        const uint32_t kk = qs_base + __umul24(min(static_cast<uint32_t>(lr), lim), kv_dim) + kcol;
+        B.kq[0] = *reinterpret_cast<const Q16*>(a.k.qs + kk);
+        B.kq[1] = *reinterpret_cast<const Q16*>(a.k.qs + (kk + 16));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t rr = min(r0 + 4u * lg + j, row_last);
+            const uint32_t y = min(4u * lg + j, lim);
             // byte offsets in 32 bits: base (SGPRs) + one VGPR offset per load
-            const uint32_t doff = (rr * nb_row + dcol) * 4u;
+            const uint32_t doff = (d_base + __umul24(y, nb_row) + dcol) * 4u;
             B.kd[j] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.k.d) + doff);
             B.vd[j] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v.d) + doff);
-            B.vv[j] = *reinterpret_cast<const u32x2*>(a.v.qs + (rr * kv_dim + vcol));
+            B.vv[j] = *reinterpret_cast<const u32x2*>(a.v.qs + (qs_base + __umul24(y, kv_dim) + vcol));
         }
     };
     const uint32_t n_rows = row_end - row0;

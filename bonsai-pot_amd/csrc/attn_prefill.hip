@@ -157,10 +157,9 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
     const int t = threadIdx.x;
-    // 1-D grid, KV head fastest (as in prefill_kernel): head g's chunks are
-    // written on the XCD whose L2 serves head g in the attention pass.
-    const uint32_t nkv = a.kv_dim / kHeadDim;
-    const uint32_t g = blockIdx.x % nkv, c = blockIdx.x / nkv;
+    // Grid (KV head, chunk), KV head fastest (as in prefill_kernel): head g's
+    // chunks are written on the XCD whose L2 serves head g in the attention pass.
+    const uint32_t g = blockIdx.x, c = blockIdx.y;
     const uint32_t nb_row = a.kv_dim / kBlock;
     const uint32_t last = a.n_rows - 1;
     // ---- loads (unconditional, clamped rows; rows past n_rows get d = 0) ----
@@ -249,7 +248,8 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
 template <int kHpw>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     constexpr int kHeadsPerWave = kHpw;
-    constexpr int kHeadSets = 2 / kHpw;
+    constexpr int kHeadSets = 2 / kHpw;   // the grid's y extent (query-head sets per KV head)
+    static_assert(kHeadSets * kHpw == 2, "two query heads per wave pair");
     // lds[stream][buf]: staged chunk (K rows, V^T rows, K residual rows), 2
     // streams x 2 buffers (160 KB, all of the CU's LDS).
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
@@ -258,12 +258,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int lane = t & 63, wave = t >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const bool is_b = (wave & 4) != 0;               // B wave (heavy tile) or A wave
-    // 1-D grid, KV head fastest: workgroups are dealt to the 8 XCDs round-robin,
-    // so with 8 KV heads each XCD serves one head and its L2 holds that head's
-    // K/V for all the head's tile pairs.
-    const uint32_t nkv = a.kv_dim / kHeadDim;
-    const uint32_t g = blockIdx.x % nkv, rest = blockIdx.x / nkv;
-    const uint32_t hs = rest % kHeadSets, pair = rest / kHeadSets;
+    // Grid (KV head, head set, tile pair), KV head fastest: workgroups are
+    // dealt to the 8 XCDs round-robin by linear id (x fastest), so with 8 KV
+    // heads each XCD serves one head and its L2 holds that head's K/V for all
+    // the head's tile pairs. (Grid dimensions instead of a 1-D id: no integer
+    // divisions at the kernel's start.)
+    const uint32_t g = blockIdx.x, hs = blockIdx.y, pair = blockIdx.z;
     const uint32_t tile_a = pair, tile_b = a.n_tiles - 1 - pair;   // tile_b >= tile_a
     const uint32_t h0 = g * kGroup + 2 * hs + kHeadsPerWave * ((wave >> 1) & 1);   // first query head
     const uint32_t utok = 16 * (wave & 1);            // unit's first token within its tile
@@ -576,12 +576,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 }  // namespace
 
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(kv_dequant_kernel, dim3((a.n_rows + kChunk - 1) / kChunk * n_kv_head), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(kv_dequant_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk), dim3(256), 0, s, a);
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
     if (a.heads_per_wave == 1)
-        hipLaunchKernelGGL(prefill_kernel<1>, dim3(2 * n_pairs * n_kv_head), dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL(prefill_kernel<1>, dim3(n_kv_head, 2, n_pairs), dim3(kThreads), 0, s, a);
     else
-        hipLaunchKernelGGL(prefill_kernel<2>, dim3(n_pairs * n_kv_head), dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL(prefill_kernel<2>, dim3(n_kv_head, 1, n_pairs), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

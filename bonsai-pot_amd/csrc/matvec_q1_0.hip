@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kMvMaxThreads) void matvec_q1_0_kernel(MatvecArgs a
     extern __shared__ __attribute__((aligned(16))) uint16_t x_sh[];
     __shared__ float red_sh[4];
     const int t = threadIdx.x, n_thr = blockDim.x;
-    const int lane = t & 63, wave = t >> 6, n_wave = n_thr >> 6;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), n_wave = n_thr >> 6;
     const uint32_t k = a.k, nb = k / kQ1Block;
     const uint32_t rows = a.rows_per_wg;
     float* terms = reinterpret_cast<float*>(x_sh + nb * kBlockHalves);   // [rows][nb]
@@ -155,7 +155,11 @@ __global__ __launch_bounds__(kMvMaxThreads) void matvec_q1_0_kernel(MatvecArgs a
 
     const uint32_t tcols = (nb + 3) / 4;
     const uint32_t n_tiles = (rows / 8) * tcols;
-    TilePos pos = {static_cast<uint32_t>(wave), static_cast<uint32_t>(wave) / tcols, static_cast<uint32_t>(wave) % tcols};
+    TilePos pos = {static_cast<uint32_t>(wave), 0u, static_cast<uint32_t>(wave)};   // (rq, col) = divmod(wave, tcols)
+    while (pos.col >= tcols) {   // no division: wave < 16, usually < tcols
+        pos.col -= tcols;
+        ++pos.rq;
+    }
     WTile cur = load_tile(a, pos, n_tiles, nb, n_here, rbase, d_off, qs_off, lane);   // in flight during pass 1
 
     // ---- pass 1: stage x (f16) into LDS, 8 elements at a time --------------------
@@ -219,10 +223,10 @@ __global__ __launch_bounds__(kMvMaxThreads) void matvec_q1_0_kernel(MatvecArgs a
         const WTile nxt = load_tile(a, nxt_pos, n_tiles, nb, n_here, rbase, d_off, qs_off, lane);
         const uint32_t r = pos.rq * 8 + (lane >> 3), b = min(pos.col * 4 + ((lane >> 1) & 3), nb - 1);
         const uint32_t q[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
-        // both lanes of a pair are valid or invalid together; a shuffle is
+        // both lanes of a pair are valid or invalid together; the lane exchange is
         // executed by all lanes
         const h2v c = q1_half(q, x_sh + b * kBlockHalves + h * kHalfStride, h);
-        const h2v c23 = __builtin_bit_cast(h2v, __shfl_xor(__builtin_bit_cast(int, c), 1));
+        const h2v c23 = __builtin_bit_cast(h2v, lane_xor<1>(__builtin_bit_cast(uint32_t, c)));
         if (cur.ok && h == 0) {
             const _Float16 sum = ((c.x + c.y) + c23.x) + c23.y;   // f16 adds, in this order
             float d = static_cast<float>(__builtin_bit_cast(_Float16, cur.d));
@@ -240,9 +244,9 @@ __global__ __launch_bounds__(kMvMaxThreads) void matvec_q1_0_kernel(MatvecArgs a
         float acc = 0.0f;
         if (r < n_here)
             for (uint32_t b = bt; b < nb; b += 8) acc = acc + terms[r * nb + b];
-        acc = acc + __shfl_xor(acc, 1);
-        acc = acc + __shfl_xor(acc, 2);
-        acc = acc + __shfl_xor(acc, 4);
+        acc = acc + lane_xor<1>(acc);
+        acc = acc + lane_xor<2>(acc);
+        acc = acc + lane_xor<4>(acc);
         if (bt == 0 && r < n_here) {
             uint16_t* y = a.act + out_off + rbase + r;
             if (kMode != 2 && a.accumulate) *y = f2h(h2f(*y) + acc);

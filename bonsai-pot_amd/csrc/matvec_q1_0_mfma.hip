@@ -238,10 +238,10 @@ __global__ __launch_bounds__(kMfMaxThreads) __attribute__((amdgpu_waves_per_eu(k
             amax = fmaxf(amax, fabsf(xf[i]));
         }
         // the 16 threads of a block are 16 consecutive lanes
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
-        amax = fmaxf(amax, __shfl_xor(amax, 4));
-        amax = fmaxf(amax, __shfl_xor(amax, 8));
+        amax = fmaxf(amax, lane_xor<1>(amax));
+        amax = fmaxf(amax, lane_xor<2>(amax));
+        amax = fmaxf(amax, lane_xor<4>(amax));
+        amax = fmaxf(amax, lane_xor<8>(amax));
         const float qs = amax > 0.0f ? kQMax / amax : 0.0f;
         const uint32_t b = v / 16, w = (v % 16) / 4, kk = v % 4;
         uint8_t* fb = sh + L.frag + b * kBlockFragBytes;   // [h][s][16]
@@ -263,10 +263,10 @@ __global__ __launch_bounds__(kMfMaxThreads) __attribute__((amdgpu_waves_per_eu(k
                     *reinterpret_cast<uint2*>(fb + h * kRunBytes + (4 * w + s2) * kFragBytes + (8 - half)) =
                         make_uint2(0u, 0u);
         }
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        sum += __shfl_xor(sum, 4);
-        sum += __shfl_xor(sum, 8);
+        sum += static_cast<int32_t>(lane_xor<1>(static_cast<uint32_t>(sum)));
+        sum += static_cast<int32_t>(lane_xor<2>(static_cast<uint32_t>(sum)));
+        sum += static_cast<int32_t>(lane_xor<4>(static_cast<uint32_t>(sum)));
+        sum += static_cast<int32_t>(lane_xor<8>(static_cast<uint32_t>(sum)));
         if ((v % 16) == 0) {
             s_int[b] = sum;
             scl[b] = amax / kQMax;

@@ -140,30 +140,56 @@ __device__ void replay_thread(const uint32_t* words, uint32_t n, uint32_t t, flo
     }
 }
 
+// Value of lane (lane ^ 16) / (lane ^ 32): v_permlane16/32_swap of a
+// register with itself leaves the partner's value in one of its two results,
+// which one depending on the lane's 16-lane (32-lane) row.
+__device__ __forceinline__ uint32_t xor16_lane(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return (__lane_id() & 16) ? r0 : r1;
+}
+__device__ __forceinline__ uint32_t xor32_lane(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return (__lane_id() & 32) ? r0 : r1;
+}
+// Value of lane 63 - lane: DPP row mirror (15 - lane within 16 lanes), then
+// the rows reversed (lane ^ 48).
+__device__ __forceinline__ uint32_t rev_lane(uint32_t v) {
+    const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x140, 0xF, 0xF, true));
+    return xor16_lane(xor32_lane(m));
+}
+
 // Value of lane (lane ^ S): DPP lane moves for S = 1, 2, 4, 8 (quad
-// permutes, half-row mirror + quad permute, row rotation by 8), a permute
-// through the LDS crossbar for 16.
+// permutes, half-row mirror + quad permute, row rotation by 8), a row swap
+// for 16.
 template <int S>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
     const int x = static_cast<int>(v);
-    if constexpr (S == 1) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
-    else if constexpr (S == 2) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    // (every source lane exists: bound_ctrl, no old value to preset)
+    if constexpr (S == 1) return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true));
+    else if constexpr (S == 2) return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true));
     else if constexpr (S == 4) {
-        const int m = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);   // lane ^ 7
-        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false));   // ^ 3
-    } else if constexpr (S == 8) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
-    else return static_cast<uint32_t>(__shfl_xor(x, S));
+        const int m = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true);   // lane ^ 7
+        return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(m, 0x1B, 0xF, 0xF, true));   // ^ 3
+    } else if constexpr (S == 8) return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true));
+    else return xor16_lane(v);
 }
 
 // One strict compare-swap stage of stride S (lanes l, l ^ S) on two lists.
 template <int S>
 __device__ __forceinline__ void merge_stages(float (&v)[2], uint32_t (&ix)[2], uint32_t lane) {
-    const bool lo = (lane & S) == 0;
+    const float sgn = (lane & S) == 0 ? 1.0f : -1.0f;
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const float pv = __builtin_bit_cast(float, xor_lane<S>(__builtin_bit_cast(uint32_t, v[u])));
         const uint32_t pi = xor_lane<S>(ix[u]);
-        const bool take = lo ? (pv > v[u]) : (v[u] > pv);   // reference: if v[hi] > v[lo] swap
+        // reference: if v[hi] > v[lo] swap, i.e. take the partner's entry if
+        // it is strictly larger (lo lane) or strictly smaller (hi lane). As one
+        // compare of the signed difference: list values are f16 values, +-inf
+        // or the -1e30 fill, so pv - v is 0 or NaN (inf - inf) exactly when no
+        // swap is due and never rounds to 0 otherwise.
+        const bool take = (pv - v[u]) * sgn > 0.0f;
         v[u] = take ? pv : v[u];
         ix[u] = take ? pi : ix[u];
     }
@@ -303,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
             hm = __builtin_elementwise_max(hm, gm);
             const uint32_t g = r * per_round + u * kThreads + tid;
             const _Float16 g0 = gm.x, g1 = gm.y;   // (scalars before the cast)
-            if (g < kGmaxCap) sh.gmax[g] = g0 > g1 ? g0 : g1;
+            if (n_rounds > 1 && g < kGmaxCap) sh.gmax[g] = g0 > g1 ? g0 : g1;
         }
     }
     uint32_t mk = 0;
@@ -320,25 +346,16 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     // fewer than 32 maxima, every insertable element is gathered
     uint32_t tau = select_key(sh, mk, kK - 1);
     if (tau == 0) tau = hkey(0xFBFFu);   // -65504, the smallest insertable value
-    const float tau_f = h2f(unkey16(tau));
 
     // ---- 2. gather the elements >= tau (few on real logits): one LDS atomic
     // per 8-element group that holds any; past kCap every heap is replayed
-    auto take = [&](uint16_t h) { return insertable(h) && hkey(h) >= tau; };
+    // (an f16 compare with tau's value is the same test: NaN fails it, and -inf
+    // is below every tau; -0 and +0 compare equal as their keys do)
+    const _Float16 tau_h = __builtin_bit_cast(_Float16, unkey16(tau));
+    auto take = [&](uint16_t h) { return __builtin_bit_cast(_Float16, h) >= tau_h; };
     // groups whose maximum reaches tau (maxima from LDS up to kGmaxCap groups,
     // recomputed beyond), then their elements
-#pragma unroll 1
-    for (uint32_t g = tid; g < n_groups; g += kThreads) {
-        float gmf;
-        if (g < kGmaxCap) {
-            gmf = static_cast<float>(sh.gmax[g]);
-        } else {
-            const h2 gm = group_max(groups[g]);
-            const _Float16 g0 = gm.x, g1 = gm.y;
-            gmf = fmaxf(static_cast<float>(g0), static_cast<float>(g1));
-        }
-        if (!(gmf >= tau_f)) continue;
-        const uint4 qg = groups[g];
+    auto gather_group = [&](const uint4& qg, uint32_t g) __attribute__((always_inline)) {
         const uint32_t w[4] = {qg.x, qg.y, qg.z, qg.w};
         uint32_t m = 0;
 #pragma unroll
@@ -349,6 +366,23 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
             const int e = __builtin_ctz(m);
             const uint16_t h = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
             if (slot < kCap) sh.cand[slot] = make_uint2(__builtin_bit_cast(uint32_t, h2f(h)), head + 8 * g + e);
+        }
+    };
+    auto gmax_h = [](const uint4& qg) {   // maxNum: NaN only for an all-NaN group
+        const h2 gm = group_max(qg);
+        const _Float16 g0 = gm.x, g1 = gm.y;
+        return g0 > g1 ? g0 : g1;
+    };
+    if (n_rounds == 1) {
+        // the only round is still in registers (groups past the end hold -inf)
+#pragma unroll
+        for (uint32_t u = 0; u < kRegGroups; u++)
+            if (gmax_h(q[u]) >= tau_h) gather_group(q[u], u * kThreads + tid);
+    } else {
+#pragma unroll 1
+        for (uint32_t g = tid; g < n_groups; g += kThreads) {
+            const _Float16 gm = g < kGmaxCap ? sh.gmax[g] : gmax_h(groups[g]);
+            if (gm >= tau_h) gather_group(groups[g], g);
         }
     }
     if (wave == 0) {   // head and tail elements
@@ -444,15 +478,23 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     // never wins the strict compares) leaves the first one unchanged and is
     // skipped. A wave runs its merges of a level (up to 8) side by side so that
     // their lane-exchange chains overlap.
+    // Which lists hold anything but fill, as a 256-bit mask in scalar registers
+    // that every wave keeps up to date itself (list p absorbs list p + s).
+    uint64_t dm0 = __ballot(sh.dirty[lane] != 0), dm1 = __ballot(sh.dirty[64 + lane] != 0),
+             dm2 = __ballot(sh.dirty[128 + lane] != 0), dm3 = __ballot(sh.dirty[192 + lane] != 0);
+    auto dirty_bit = [&](uint32_t i) {
+        const uint64_t w = i < 64 ? dm0 : i < 128 ? dm1 : i < 192 ? dm2 : dm3;
+        return ((w >> (i & 63)) & 1u) != 0;
+    };
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll 1
     for (uint32_t s = kLanes / 2; s > 0; s /= 2) {
         uint32_t need = 0;   // bit u: merge p = wave + 16 u runs
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const uint32_t p = wave + kWaves * u;
-            if (p < s && (s == 1 || sh.dirty[p + s])) need |= 1u << u;
+            const uint32_t p = wv + kWaves * u;
+            if (p < s && (s == 1 || dirty_bit(p + s))) need |= 1u << u;
         }
-        need = __builtin_amdgcn_readfirstlane(need);   // uniform: p depends on the wave only
 #pragma unroll 1
         for (int u0 = 0; u0 < 8; u0 += 2) {
             const uint32_t nd = (need >> u0) & 3u;
@@ -461,14 +503,14 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
             uint32_t ix[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t p = wave + kWaves * (u0 + u);
+                const uint32_t p = wv + kWaves * (u0 + u);
                 const uint2 xv = (nd >> u) & 1u ? sh.lists[(lane < kK ? p : p + s) * kK + (lane & (kK - 1))]
                                                 : make_uint2(__builtin_bit_cast(uint32_t, kEmpty), 0u);
                 // stage 0: a[i] = b[31 - i] if strictly greater (b[31 - i] sits in lane 63 - i)
                 v[u] = __builtin_bit_cast(float, xv.x);
                 ix[u] = xv.y;
-                const float bv = __shfl(v[u], 63 - lane);
-                const uint32_t bi = __shfl(ix[u], 63 - lane);
+                const float bv = __builtin_bit_cast(float, rev_lane(xv.x));
+                const uint32_t bi = rev_lane(ix[u]);
                 if (bv > v[u]) { v[u] = bv; ix[u] = bi; }
             }
             merge_stages<16>(v, ix, lane);
@@ -479,10 +521,9 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 if (!((nd >> u) & 1u)) continue;
-                const uint32_t p = wave + kWaves * (u0 + u);
+                const uint32_t p = wv + kWaves * (u0 + u);
                 if (s > 1) {
                     if (lane < kK) sh.lists[p * kK + lane] = make_uint2(__builtin_bit_cast(uint32_t, v[u]), ix[u]);
-                    if (lane == 0) sh.dirty[p] = 1;
                 } else {
                     const uint32_t kk = a.k < kK ? a.k : kK;
                     if (lane < kk) {
@@ -492,6 +533,9 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
                 }
             }
         }
+        if (s == 128) { dm0 |= dm2; dm1 |= dm3; }
+        else if (s == 64) dm0 |= dm1;
+        else dm0 |= dm0 >> s;   // bits past s are not read again
         __syncthreads();
     }
 }

@@ -224,6 +224,8 @@ struct TopKShared {
     uint32_t replay[kLanes];    // per reference thread: 1 = replay its heap
     uint32_t replay_ids[kLanes];
     uint32_t dirty[kLanes];     // list holds anything but the -1e30 / 0 fill
+    uint32_t tcnt[kLanes];      // bigs per reference thread (one-wave case)
+    float cval[64];             // candidate values (one-wave case)
     uint32_t n_cand, n_replay, sel_hi, sel_rank, tau_key;
 };
 
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     if (tid == 0) { sh.n_cand = 0; sh.n_replay = 0; }
     for (uint32_t i = tid; i < kLanes * kK; i += kThreads)
         sh.lists[i] = make_uint2(__builtin_bit_cast(uint32_t, kEmpty), 0u);
-    if (tid < kLanes) { sh.replay[tid] = 0; sh.dirty[tid] = 0; }
+    if (tid < kLanes) { sh.replay[tid] = 0; sh.dirty[tid] = 0; sh.tcnt[tid] = 0; }
 
     // ---- 1. per-thread maximum key of the insertable values. The groups are
     // taken kRegGroups per thread at a time into registers (all loads in
@@ -397,25 +399,40 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     const uint32_t n_cand = sh.n_cand;
     const bool overflow = n_cand > kCap;
     if (!overflow && n_cand <= 64) {
-        // one wave: lane i holds candidate i; the others' values by readlane
+        // one wave: lane i holds candidate i
         if (wave == 0) {
             const bool live = lane < n_cand;
             const uint2 c = live ? sh.cand[lane] : make_uint2(__builtin_bit_cast(uint32_t, kEmpty), 0u);
             const float vi = __builtin_bit_cast(float, c.x);
             const uint32_t ti = (c.y >> 1) & (kLanes - 1);
-            uint32_t g = 0;
-            for (uint32_t j = 0; j < n_cand; j++) g += rl(vi, j) > vi;
+            // g = the number of larger candidates, from the 64 values (padded
+            // with -1e30, which is below every candidate) broadcast from LDS
+            sh.cval[lane] = vi;
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_wave_barrier();
+            uint32_t gp[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 64; j++) gp[j & 3] += sh.cval[j] > vi;
+            const uint32_t g = (gp[0] + gp[1]) + (gp[2] + gp[3]);
             const bool big = live && g < kK;
-            const uint64_t bigm = __ballot(big);
+            // r = the larger bigs of the same reference thread; only threads
+            // holding two or more bigs (counted in LDS) need the comparison
+            if (big) atomicAdd(&sh.tcnt[ti], 1u);
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_wave_barrier();
+            const bool coll = big && sh.tcnt[ti] > 1;
+            uint64_t collm = __ballot(coll);
             uint32_t r = 0;
             bool dup = false;
-            for (uint32_t j = 0; j < n_cand; j++) {
-                if (!((bigm >> j) & 1u)) continue;
+            while (collm) {
+                const uint32_t j = __builtin_ctzll(collm);
+                collm &= collm - 1;
                 const float vj = rl(vi, j);
                 const uint32_t tj = rl(ti, j);
-                if (j == lane || tj != ti) continue;
-                r += vj > vi;
-                dup = dup || vj == vi;
+                if (coll && j != lane && tj == ti) {
+                    r += vj > vi;
+                    dup = dup || vj == vi;
+                }
             }
             if (big && (dup || r >= kK)) sh.replay[ti] = 1;
             __builtin_amdgcn_s_waitcnt(0);

@@ -176,12 +176,12 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
     else return xor16_lane(v);
 }
 
-// One strict compare-swap stage of stride S (lanes l, l ^ S) on two lists.
-template <int S>
-__device__ __forceinline__ void merge_stages(float (&v)[2], uint32_t (&ix)[2], uint32_t lane) {
+// One strict compare-swap stage of stride S (lanes l, l ^ S) on N lists.
+template <int S, int N>
+__device__ __forceinline__ void merge_stages(float (&v)[N], uint32_t (&ix)[N], uint32_t lane) {
     const float sgn = (lane & S) == 0 ? 1.0f : -1.0f;
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+    for (int u = 0; u < N; u++) {
         const float pv = __builtin_bit_cast(float, xor_lane<S>(__builtin_bit_cast(uint32_t, v[u])));
         const uint32_t pi = xor_lane<S>(ix[u]);
         // reference: if v[hi] > v[lo] swap, i.e. take the partner's entry if
@@ -192,6 +192,45 @@ __device__ __forceinline__ void merge_stages(float (&v)[2], uint32_t (&ix)[2], u
         const bool take = (pv - v[u]) * sgn > 0.0f;
         v[u] = take ? pv : v[u];
         ix[u] = take ? pi : ix[u];
+    }
+}
+
+// N merges of one tree level run side by side by one wave, so that their
+// lane-exchange chains overlap: list p[u] absorbs list p[u] + s (list p in
+// lanes 0..31, list p + s in lanes 32..63).
+template <int N>
+__device__ __forceinline__ void merge_lists(uint2* lists, const uint32_t (&p)[N], uint32_t s, uint32_t lane,
+                                            uint32_t* result, uint32_t out_offset, uint32_t kk) {
+    float v[N];
+    uint32_t ix[N];
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+        const uint2 xv = lists[(lane < kK ? p[u] : p[u] + s) * kK + (lane & (kK - 1))];
+        v[u] = __builtin_bit_cast(float, xv.x);
+        ix[u] = xv.y;
+    }
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+        // stage 0: a[i] = b[31 - i] if strictly greater (b[31 - i] sits in lane 63 - i)
+        const float bv = __builtin_bit_cast(float, rev_lane(__builtin_bit_cast(uint32_t, v[u])));
+        const uint32_t bi = rev_lane(ix[u]);
+        const bool take = bv > v[u];
+        v[u] = take ? bv : v[u];
+        ix[u] = take ? bi : ix[u];
+    }
+    merge_stages<16, N>(v, ix, lane);
+    merge_stages<8, N>(v, ix, lane);
+    merge_stages<4, N>(v, ix, lane);
+    merge_stages<2, N>(v, ix, lane);
+    merge_stages<1, N>(v, ix, lane);
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+        if (s > 1) {
+            if (lane < kK) lists[p[u] * kK + lane] = make_uint2(__builtin_bit_cast(uint32_t, v[u]), ix[u]);
+        } else if (lane < kk) {
+            result[out_offset + lane] = __builtin_bit_cast(uint32_t, v[u]);
+            result[out_offset + kk + lane] = ix[u];
+        }
     }
 }
 
@@ -229,6 +268,20 @@ struct TopKShared {
     uint32_t n_cand, n_replay, sel_hi, sel_rank, tau_key;
 };
 
+// Inclusive prefix sum over the 64 lanes: within each 16-lane row by DPP row
+// shifts (lanes without a source add 0), then the totals of the rows below
+// (read from lanes 15, 31, 47) added per row.
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xF, 0xF, true));   // row_shr:1
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xF, 0xF, true));   // row_shr:2
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xF, 0xF, true));   // row_shr:4
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xF, 0xF, true));   // row_shr:8
+    const uint32_t t0 = rl(v, 15), t1 = rl(v, 31), t2 = rl(v, 47);
+    const uint32_t row = __lane_id() >> 4;
+    const uint32_t below = (row >= 1 ? t0 : 0u) + (row >= 2 ? t1 : 0u) + (row >= 3 ? t2 : 0u);
+    return v + below;
+}
+
 // Key of the rank-th largest (0-based) of the 1024 keys held one per thread
 // (0 = no value), by two 8-bit radix rounds; 0 if fewer than rank + 1 keys.
 __device__ uint32_t select_key(TopKShared& sh, uint32_t key, uint32_t rank) {
@@ -238,26 +291,14 @@ __device__ uint32_t select_key(TopKShared& sh, uint32_t key, uint32_t rank) {
         __syncthreads();
         const bool in = key != 0 && (round == 0 || (key >> 8) == sh.sel_hi);
         const uint32_t bin = round == 0 ? key >> 8 : key & 0xFFu;
-        // one atomic per distinct bin of the wave (the keys crowd into few bins)
-        uint64_t left = __ballot(in);
-        while (left) {
-            const uint32_t b = __builtin_amdgcn_readlane(bin, __builtin_ctzll(left));
-            const uint64_t same = __ballot(in && bin == b) & left;
-            if ((threadIdx.x & 63) == __builtin_ctzll(same)) atomicAdd(&sh.hist[b], static_cast<uint32_t>(__popcll(same)));
-            left &= ~same;
-        }
+        if (in) atomicAdd(&sh.hist[bin], 1u);   // same-bin lanes serialize inside the LDS
         __syncthreads();
         if (tid < 64) {   // one wave scans the bins from the top
             const uint32_t want = round == 0 ? rank : sh.sel_rank;
             uint32_t c[4], tot = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) { c[i] = sh.hist[255 - (4 * tid + i)]; tot += c[i]; }
-            uint32_t incl = tot;   // inclusive prefix over lanes (bins from the top)
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t o = __shfl_up(incl, off);
-                if (tid >= static_cast<uint32_t>(off)) incl += o;
-            }
+            const uint32_t incl = wave_incl_sum(tot);   // inclusive prefix over lanes (bins from the top)
             uint32_t run = incl - tot;
             bool found = false;
             uint32_t bin = 0, above = 0;
@@ -499,55 +540,41 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     // that every wave keeps up to date itself (list p absorbs list p + s).
     uint64_t dm0 = __ballot(sh.dirty[lane] != 0), dm1 = __ballot(sh.dirty[64 + lane] != 0),
              dm2 = __ballot(sh.dirty[128 + lane] != 0), dm3 = __ballot(sh.dirty[192 + lane] != 0);
-    auto dirty_bit = [&](uint32_t i) {
-        const uint64_t w = i < 64 ? dm0 : i < 128 ? dm1 : i < 192 ? dm2 : dm3;
-        return ((w >> (i & 63)) & 1u) != 0;
-    };
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll 1
     for (uint32_t s = kLanes / 2; s > 0; s /= 2) {
-        uint32_t need = 0;   // bit u: merge p = wave + 16 u runs
+        // bit u: merge p = wave + 16 u runs (p < s and list p + s dirty; at
+        // s = 1 always, to write the result). Bits of the lists p + s = wave +
+        // s + 16 u, gathered from the mask without branches.
+        uint32_t need = 0;
+        if (s == 1) {
+            need = wv == 0 ? 1u : 0u;
+        } else if (s >= 16) {
+            const uint32_t i0 = wv + s;   // list of u = 0; u < s / 16 are in range
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t p = wv + kWaves * u;
-            if (p < s && (s == 1 || dirty_bit(p + s))) need |= 1u << u;
-        }
-#pragma unroll 1
-        for (int u0 = 0; u0 < 8; u0 += 2) {
-            const uint32_t nd = (need >> u0) & 3u;
-            if (!nd) continue;
-            float v[2];
-            uint32_t ix[2];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t p = wv + kWaves * (u0 + u);
-                const uint2 xv = (nd >> u) & 1u ? sh.lists[(lane < kK ? p : p + s) * kK + (lane & (kK - 1))]
-                                                : make_uint2(__builtin_bit_cast(uint32_t, kEmpty), 0u);
-                // stage 0: a[i] = b[31 - i] if strictly greater (b[31 - i] sits in lane 63 - i)
-                v[u] = __builtin_bit_cast(float, xv.x);
-                ix[u] = xv.y;
-                const float bv = __builtin_bit_cast(float, rev_lane(xv.x));
-                const uint32_t bi = rev_lane(ix[u]);
-                if (bv > v[u]) { v[u] = bv; ix[u] = bi; }
+            for (int u = 0; u < 8; u++) {
+                const uint32_t i = i0 + kWaves * u;
+                const uint64_t w = i < 64 ? dm0 : i < 128 ? dm1 : i < 192 ? dm2 : dm3;
+                need |= static_cast<uint32_t>((w >> (i & 63)) & 1u) << u;
             }
-            merge_stages<16>(v, ix, lane);
-            merge_stages<8>(v, ix, lane);
-            merge_stages<4>(v, ix, lane);
-            merge_stages<2>(v, ix, lane);
-            merge_stages<1>(v, ix, lane);
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                if (!((nd >> u) & 1u)) continue;
-                const uint32_t p = wv + kWaves * (u0 + u);
-                if (s > 1) {
-                    if (lane < kK) sh.lists[p * kK + lane] = make_uint2(__builtin_bit_cast(uint32_t, v[u]), ix[u]);
-                } else {
-                    const uint32_t kk = a.k < kK ? a.k : kK;
-                    if (lane < kk) {
-                        a.result[a.out_offset + lane] = __builtin_bit_cast(uint32_t, v[u]);
-                        a.result[a.out_offset + kk + lane] = ix[u];
-                    }
-                }
+            need &= (1u << (s / kWaves)) - 1u;
+        } else {
+            need = wv < s ? static_cast<uint32_t>((dm0 >> (wv + s)) & 1u) : 0u;
+        }
+        // the wave's merges two at a time (one if one is left)
+        const uint32_t kk = a.k < kK ? a.k : kK;
+#pragma unroll 1
+        while (need) {
+            const uint32_t u0 = __builtin_ctz(need);
+            need &= need - 1;
+            if (need) {
+                const uint32_t u1 = __builtin_ctz(need);
+                need &= need - 1;
+                const uint32_t ps[2] = {wv + kWaves * u0, wv + kWaves * u1};
+                merge_lists<2>(sh.lists, ps, s, lane, a.result, a.out_offset, kk);
+            } else {
+                const uint32_t ps[1] = {wv + kWaves * u0};
+                merge_lists<1>(sh.lists, ps, s, lane, a.result, a.out_offset, kk);
             }
         }
         if (s == 128) { dm0 |= dm2; dm1 |= dm3; }

@@ -263,6 +263,7 @@ struct TopKShared {
     uint32_t replay[kLanes];    // per reference thread: 1 = replay its heap
     uint32_t replay_ids[kLanes];
     uint32_t dirty[kLanes];     // list holds anything but the -1e30 / 0 fill
+    uint32_t multi[kLanes];     // list holds two or more entries (merge tree)
     uint32_t tcnt[kLanes];      // bigs per reference thread (one-wave case)
     float cval[64];             // candidate values (one-wave case)
     uint32_t n_cand, n_replay, sel_hi, sel_rank, tau_key;
@@ -536,40 +537,51 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     // never wins the strict compares) leaves the first one unchanged and is
     // skipped. A wave runs its merges of a level (up to 8) side by side so that
     // their lane-exchange chains overlap.
-    // Which lists hold anything but fill, as a 256-bit mask in scalar registers
-    // that every wave keeps up to date itself (list p absorbs list p + s).
-    uint64_t dm0 = __ballot(sh.dirty[lane] != 0), dm1 = __ballot(sh.dirty[64 + lane] != 0),
-             dm2 = __ballot(sh.dirty[128 + lane] != 0), dm3 = __ballot(sh.dirty[192 + lane] != 0);
+    // Per list: dirty (anything but fill) and multi (two or more entries;
+    // lists are sorted descending, so "slot 1 is not fill"), in LDS.
+    const uint32_t fill_bits = __builtin_bit_cast(uint32_t, kEmpty);
+    if (tid < kLanes) sh.multi[tid] = sh.dirty[tid] != 0 && sh.lists[tid * kK + 1].x != fill_bits ? 1u : 0u;
+    __syncthreads();
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t kk = a.k < kK ? a.k : kK;
 #pragma unroll 1
     for (uint32_t s = kLanes / 2; s > 0; s /= 2) {
-        // bit u: merge p = wave + 16 u runs (p < s and list p + s dirty; at
-        // s = 1 always, to write the result). Bits of the lists p + s = wave +
-        // s + 16 u, gathered from the mask without branches.
-        uint32_t need = 0;
-        if (s == 1) {
-            need = wv == 0 ? 1u : 0u;
-        } else if (s >= 16) {
-            const uint32_t i0 = wv + s;   // list of u = 0; u < s / 16 are in range
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const uint32_t i = i0 + kWaves * u;
-                const uint64_t w = i < 64 ? dm0 : i < 128 ? dm1 : i < 192 ? dm2 : dm3;
-                need |= static_cast<uint32_t>((w >> (i & 63)) & 1u) << u;
+        if (wv >= s) return;   // no merges left for this wave (ended waves leave the barriers)
+        // Lane u < 8 looks at merge u of this wave: list p = wave + 16 u
+        // absorbs list p + s. With list p + s dirty it runs the network if
+        // either list holds two or more entries, and is closed-form otherwise
+        // (one entry on each side, or none in list p): the reference network
+        // leaves [x, y] if y <= x and [y, x] if y > x (x = list p's entry or
+        // fill, y = list p + s's entry). At s = 1 the network always runs (it
+        // writes the result).
+        const uint32_t pu = wv + kWaves * lane;
+        const bool valid = lane < 8 && pu < s;
+        const uint32_t dp = valid ? sh.dirty[pu] : 0u, di = valid ? sh.dirty[pu + s] : 0u;
+        const uint32_t mp = valid ? sh.multi[pu] : 0u, mi = valid ? sh.multi[pu + s] : 0u;
+        const bool merge = di != 0 || (s == 1 && valid);
+        const bool use_net = merge && (mp != 0 || mi != 0 || s == 1);
+        uint32_t net = static_cast<uint32_t>(__ballot(use_net)) & 0xFFu;
+        if (merge && !use_net) {   // closed-form
+            const uint2 x = sh.lists[pu * kK], y = sh.lists[(pu + s) * kK];
+            if (__builtin_bit_cast(float, y.x) > __builtin_bit_cast(float, x.x)) {
+                sh.lists[pu * kK] = y;
+                sh.lists[pu * kK + 1] = x;
+            } else {
+                sh.lists[pu * kK + 1] = y;
             }
-            need &= (1u << (s / kWaves)) - 1u;
-        } else {
-            need = wv < s ? static_cast<uint32_t>((dm0 >> (wv + s)) & 1u) : 0u;
         }
-        // the wave's merges two at a time (one if one is left)
-        const uint32_t kk = a.k < kK ? a.k : kK;
+        if (merge) {   // flags of the merged list (list p + s is not read again)
+            sh.dirty[pu] = 1u;
+            sh.multi[pu] = mp != 0 || mi != 0 || dp != 0 ? 1u : 0u;
+        }
+        // network merges two at a time (one if one is left)
 #pragma unroll 1
-        while (need) {
-            const uint32_t u0 = __builtin_ctz(need);
-            need &= need - 1;
-            if (need) {
-                const uint32_t u1 = __builtin_ctz(need);
-                need &= need - 1;
+        while (net) {
+            const uint32_t u0 = __builtin_ctz(net);
+            net &= net - 1;
+            if (net) {
+                const uint32_t u1 = __builtin_ctz(net);
+                net &= net - 1;
                 const uint32_t ps[2] = {wv + kWaves * u0, wv + kWaves * u1};
                 merge_lists<2>(sh.lists, ps, s, lane, a.result, a.out_offset, kk);
             } else {
@@ -577,9 +589,6 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
                 merge_lists<1>(sh.lists, ps, s, lane, a.result, a.out_offset, kk);
             }
         }
-        if (s == 128) { dm0 |= dm2; dm1 |= dm3; }
-        else if (s == 64) dm0 |= dm1;
-        else dm0 |= dm0 >> s;   // bits past s are not read again
         __syncthreads();
     }
 }

@@ -198,16 +198,17 @@ __device__ __forceinline__ void merge_stages(float (&v)[N], uint32_t (&ix)[N], u
 // N merges of one tree level run side by side by one wave, so that their
 // lane-exchange chains overlap: list p[u] absorbs list p[u] + s (list p in
 // lanes 0..31, list p + s in lanes 32..63).
+// (merge_lists_loaded: the lane's entries of the two lists already loaded)
 template <int N>
-__device__ __forceinline__ void merge_lists(uint2* lists, const uint32_t (&p)[N], uint32_t s, uint32_t lane,
-                                            uint32_t* result, uint32_t out_offset, uint32_t kk) {
+__device__ __forceinline__ void merge_lists_loaded(uint2* lists, const uint32_t (&p)[N], const uint2 (&xv)[N],
+                                                   uint32_t s, uint32_t lane, uint32_t* result, uint32_t out_offset,
+                                                   uint32_t kk) {
     float v[N];
     uint32_t ix[N];
 #pragma unroll
     for (int u = 0; u < N; u++) {
-        const uint2 xv = lists[(lane < kK ? p[u] : p[u] + s) * kK + (lane & (kK - 1))];
-        v[u] = __builtin_bit_cast(float, xv.x);
-        ix[u] = xv.y;
+        v[u] = __builtin_bit_cast(float, xv[u].x);
+        ix[u] = xv[u].y;
     }
 #pragma unroll
     for (int u = 0; u < N; u++) {
@@ -232,6 +233,15 @@ __device__ __forceinline__ void merge_lists(uint2* lists, const uint32_t (&p)[N]
             result[out_offset + kk + lane] = ix[u];
         }
     }
+}
+
+template <int N>
+__device__ __forceinline__ void merge_lists(uint2* lists, const uint32_t (&p)[N], uint32_t s, uint32_t lane,
+                                            uint32_t* result, uint32_t out_offset, uint32_t kk) {
+    uint2 xv[N];
+#pragma unroll
+    for (int u = 0; u < N; u++) xv[u] = lists[(lane < kK ? p[u] : p[u] + s) * kK + (lane & (kK - 1))];
+    merge_lists_loaded<N>(lists, p, xv, s, lane, result, out_offset, kk);
 }
 
 // 16-bit key with the order of the f16 values (-0 and +0 share a key).
@@ -554,6 +564,10 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
         // leaves [x, y] if y <= x and [y, x] if y > x (x = list p's entry or
         // fill, y = list p + s's entry). At s = 1 the network always runs (it
         // writes the result).
+        // (from s = 16 on a wave has one merge, p = wave: its lists are read
+        // in the same round trip as the flags)
+        uint2 pre[1];
+        if (s <= kWaves) pre[0] = sh.lists[(lane < kK ? wv : wv + s) * kK + (lane & (kK - 1))];
         const uint32_t pu = wv + kWaves * lane;
         const bool valid = lane < 8 && pu < s;
         const uint32_t dp = valid ? sh.dirty[pu] : 0u, di = valid ? sh.dirty[pu + s] : 0u;
@@ -573,6 +587,13 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
         if (merge) {   // flags of the merged list (list p + s is not read again)
             sh.dirty[pu] = 1u;
             sh.multi[pu] = mp != 0 || mi != 0 || dp != 0 ? 1u : 0u;
+        }
+        if (s <= kWaves) {
+            if (net) {
+                const uint32_t ps[1] = {wv};
+                merge_lists_loaded<1>(sh.lists, ps, pre, s, lane, a.result, a.out_offset, kk);
+            }
+            net = 0;
         }
         // network merges two at a time (one if one is left)
 #pragma unroll 1

@@ -375,6 +375,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     };
     // packed f16 maximum (maxNum: NaN operands drop out; -inf is the identity)
     h2 hm = {-INFINITY, -INFINITY};
+    _Float16 gmx[kRegGroups];   // group maxima of the last round (the gather's first test)
     for (uint32_t r = 0; r < n_rounds; r++) {
         load_round(r);
 #pragma unroll
@@ -383,7 +384,8 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
             hm = __builtin_elementwise_max(hm, gm);
             const uint32_t g = r * per_round + u * kThreads + tid;
             const _Float16 g0 = gm.x, g1 = gm.y;   // (scalars before the cast)
-            if (n_rounds > 1 && g < kGmaxCap) sh.gmax[g] = g0 > g1 ? g0 : g1;
+            gmx[u] = g0 > g1 ? g0 : g1;
+            if (n_rounds > 1 && g < kGmaxCap) sh.gmax[g] = gmx[u];
         }
     }
     uint32_t mk = 0;
@@ -429,9 +431,11 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     };
     if (n_rounds == 1) {
         // the only round is still in registers (groups past the end hold -inf)
+        if (mk >= tau) {   // only threads whose maximum key reaches tau hold any
 #pragma unroll
-        for (uint32_t u = 0; u < kRegGroups; u++)
-            if (gmax_h(q[u]) >= tau_h) gather_group(q[u], u * kThreads + tid);
+            for (uint32_t u = 0; u < kRegGroups; u++)
+                if (gmx[u] >= tau_h) gather_group(q[u], u * kThreads + tid);
+        }
     } else {
 #pragma unroll 1
         for (uint32_t g = tid; g < n_groups; g += kThreads) {

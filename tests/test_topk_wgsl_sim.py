@@ -46,6 +46,28 @@ def _sift_down(val, idx, base, size):
         i = smallest
 
 
+def _merge_lists(val, idx, a_base, b_base):
+    """List a absorbs list b: stage 0 (:141-153), then the strict compare-swap
+    stages of stride 16 .. 1 (:156-181)."""
+    for i in range(K_MAX):
+        bi = K_MAX - 1 - i
+        if val[b_base + bi] > val[a_base + i]:
+            val[a_base + i] = val[b_base + bi]
+            idx[a_base + i] = idx[b_base + bi]
+    stride = K_MAX // 2
+    while stride > 0:
+        for local in range(K_MAX // 2):
+            lo = ((local & ~(stride - 1)) << 1) | (local & (stride - 1))
+            hi = lo | stride
+            vlo, vhi = val[a_base + lo], val[a_base + hi]
+            if vhi > vlo:
+                ilo = idx[a_base + lo]
+                val[a_base + lo], val[a_base + hi] = vhi, vlo
+                idx[a_base + lo] = idx[a_base + hi]
+                idx[a_base + hi] = ilo
+        stride //= 2
+
+
 def simulate(words_f16: np.ndarray, n: int, in_offset: int, k: int):
     """Returns (values as f32 bit patterns, indices) of the top-min(k, 32)."""
     halves = words_f16.view(np.float16)
@@ -82,29 +104,12 @@ def simulate(words_f16: np.ndarray, n: int, in_offset: int, k: int):
             idx[base], idx[last] = idx[last], idx[base]
             _sift_down(val, idx, base, active_minus1)
     # ---- phase 2b (:121-184): pairwise merges, s = 128 .. 1 ----
+    # (each stage's invocations touch disjoint pairs of lists, so running the
+    # merges pair by pair gives the same entries)
     s = WG // 2
     while s > 0:
-        for kk in range(s * K_MAX):            # stage 0 (:141-153)
-            pair_id, i = divmod(kk, K_MAX)
-            a_base, b_base = pair_id * K_MAX, (pair_id + s) * K_MAX
-            bi = K_MAX - 1 - i
-            if val[b_base + bi] > val[a_base + i]:
-                val[a_base + i] = val[b_base + bi]
-                idx[a_base + i] = idx[b_base + bi]
-        stride = K_MAX // 2                     # stages 1.. (:156-181)
-        while stride > 0:
-            for kk in range(s * (K_MAX // 2)):
-                pair_id, local = divmod(kk, K_MAX // 2)
-                lo = ((local & ~(stride - 1)) << 1) | (local & (stride - 1))
-                hi = lo | stride
-                a_base = pair_id * K_MAX
-                vlo, vhi = val[a_base + lo], val[a_base + hi]
-                if vhi > vlo:
-                    ilo = idx[a_base + lo]
-                    val[a_base + lo], val[a_base + hi] = vhi, vlo
-                    idx[a_base + lo] = idx[a_base + hi]
-                    idx[a_base + hi] = ilo
-            stride //= 2
+        for pair_id in range(s):
+            _merge_lists(val, idx, pair_id * K_MAX, (pair_id + s) * K_MAX)
         s //= 2
     kk = min(k, K_MAX)                          # :186-194
     vals = np.array(val[:kk], np.float32).view(np.uint32)
@@ -161,3 +166,23 @@ def test_simulation_distinct_is_sorted_topk():
     order = np.argsort(-x.astype(np.float64), kind="stable")[:32]
     assert np.array_equal(i, order)
     assert np.array_equal(v.view(np.float32), x[order].astype(np.float32))
+
+
+def test_one_entry_merge_closed_form():
+    """The kernel merges two lists of one entry each (or an empty first list
+    and a one-entry second list) without the network: [x, y] if y <= x and
+    [y, x] if y > x, fill after. Checked against the simulator's network for
+    equal values, signed zeros, infinities and the -1e30 fill as x."""
+    fill = np.float32(-1e30)
+    vals = [np.float32(v) for v in (0.0, -0.0, 1.5, -1.5, 65504.0, -65504.0, np.inf, 3.0, 3.0)]
+    for x in vals + [fill]:
+        for y in vals:
+            xi = 0 if x == fill else 1
+            val = [x] + [fill] * (K_MAX - 1) + [y] + [fill] * (K_MAX - 1)
+            ix = [xi] + [0] * (K_MAX - 1) + [2] + [0] * (K_MAX - 1)
+            _merge_lists(val, ix, 0, K_MAX)
+            want = [(y, 2), (x, xi)] if y > x else [(x, xi), (y, 2)]
+            got = [(val[0], ix[0]), (val[1], ix[1])]
+            assert [(np.float32(a).tobytes(), b) for a, b in got] == \
+                [(np.float32(a).tobytes(), b) for a, b in want], (x, y, got)
+            assert all(v == fill for v in val[2:K_MAX]) and all(i == 0 for i in ix[2:K_MAX])

@@ -155,6 +155,11 @@ def _cases():
     x[z[:30]] = 0.0
     x[z[30:]] = -0.0
     yield "signed_zeros", x, 32, 0
+    # more than 19 groups of 8 per thread: the groups are loaded in two rounds
+    # and the gather re-reads them (group maxima from LDS, then recomputed)
+    yield "two_rounds", (rng.standard_normal(200003) * 3).astype(np.float16), 32, 0
+    x = rng.integers(-20, 6, 330007).astype(np.float16)
+    yield "three_rounds_ties", x, 32, 0
 
 
 @pytest.mark.gpu

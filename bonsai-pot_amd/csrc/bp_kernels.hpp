@@ -35,6 +35,7 @@ struct QNormRopeArgs {
     uint32_t q_dim;           // n_head * 128
     float eps;
     uint32_t n_head, n_items;   // set by launch_q_norm_rope (m_tokens * n_head items)
+    uint32_t head_shift;        // set by launch_q_norm_rope: log2(n_head) if a power of two, else 32
 };
 
 struct KvWritebackArgs {
@@ -50,6 +51,7 @@ struct KvWritebackArgs {
     uint32_t kv_dim;          // n_kv_head * 128
     float eps;
     uint32_t n_kv_head, n_pairs;   // set by launch_kv_writeback (m_tokens * n_kv_head pairs)
+    uint32_t head_shift;           // set by launch_kv_writeback: log2(n_kv_head) if a power of two, else 32
 };
 
 struct DecodeArgs {

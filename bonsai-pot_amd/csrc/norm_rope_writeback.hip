@@ -119,6 +119,21 @@ __device__ __forceinline__ void quantize_store8(const float* x0, const float* x1
     }
 }
 
+// (token, head) of item i: shift and mask when the head count is a power of
+// two (a uniform branch), else an integer division.
+__device__ __forceinline__ void divmod_heads(uint32_t i, uint32_t n, uint32_t shift, uint32_t& tok, uint32_t& head) {
+    if (shift < 32) {
+        tok = i >> shift;
+        head = i & (n - 1);
+    } else {
+        tok = i / n;
+        head = i % n;
+    }
+}
+static uint32_t head_shift_of(uint32_t n) {
+    return n != 0 && (n & (n - 1)) == 0 ? static_cast<uint32_t>(__builtin_ctz(n)) : 32u;
+}
+
 // Item it = 8 (4 blockIdx.x + wave) + lane / 8 of the m_tokens x n_head
 // (token-major) grid. Items past the end compute on a clamped item and store
 // nothing (the lane exchanges need every lane of the 8-lane group).
@@ -128,7 +143,8 @@ __global__ __launch_bounds__(256) void q_norm_rope_kernel(QNormRopeArgs a) {
     const uint32_t it_raw = kItemLanes * (4 * blockIdx.x + (threadIdx.x >> 6)) + (lane >> 3);
     const bool live = it_raw < a.n_items;
     const uint32_t it = live ? it_raw : a.n_items - 1;
-    const uint32_t head = it % a.n_head, tok = it / a.n_head;
+    uint32_t head, tok;
+    divmod_heads(it, a.n_head, a.head_shift, tok, head);
     uint16_t* q = a.act + a.q_off + static_cast<uint64_t>(tok) * a.q_dim + head * kHeadDim;
     float x0[8], x1[8];
     load8<kVec>(q + 8 * L, x0);
@@ -149,7 +165,8 @@ __global__ __launch_bounds__(256) void kv_writeback_kernel(KvWritebackArgs a) {
     const uint32_t pr_raw = kItemLanes * (4 * blockIdx.x + (threadIdx.x >> 6)) + (lane >> 3);
     const bool live = pr_raw < a.n_pairs;
     const uint32_t pr = live ? pr_raw : a.n_pairs - 1;
-    const uint32_t head = pr % a.n_kv_head, tok = pr / a.n_kv_head;
+    uint32_t head, tok;
+    divmod_heads(pr, a.n_kv_head, a.head_shift, tok, head);
     const uint64_t tok_off = static_cast<uint64_t>(tok) * a.kv_dim + head * kHeadDim;
     const uint16_t* k = a.act + a.k_cur_off + tok_off;
     const uint16_t* v = a.act + a.v_cur_off + tok_off;
@@ -187,6 +204,7 @@ hipError_t launch_q_norm_rope(const QNormRopeArgs& a, uint32_t n_head, uint32_t 
     QNormRopeArgs b = a;
     b.n_head = n_head;
     b.n_items = n_head * m_tokens;
+    b.head_shift = head_shift_of(n_head);
     const dim3 grid((b.n_items + 4 * kItemLanes - 1) / (4 * kItemLanes));
     // 16-byte vectors when the caller's offsets allow them.
     if ((b.q_off | b.w_off | b.q_dim) % 8 == 0 && reinterpret_cast<uintptr_t>(b.act) % 16 == 0 &&
@@ -202,6 +220,7 @@ hipError_t launch_kv_writeback(const KvWritebackArgs& a, uint32_t n_kv_head, uin
     KvWritebackArgs b = a;
     b.n_kv_head = n_kv_head;
     b.n_pairs = n_kv_head * m_tokens;
+    b.head_shift = head_shift_of(n_kv_head);
     const dim3 grid((b.n_pairs + 4 * kItemLanes - 1) / (4 * kItemLanes));
     if ((b.k_cur_off | b.v_cur_off | b.w_off) % 8 == 0 && reinterpret_cast<uintptr_t>(b.act) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(b.w_norms) % 16 == 0)

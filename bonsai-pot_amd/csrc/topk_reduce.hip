@@ -24,22 +24,27 @@
 //
 // One 1024-thread workgroup:
 //  1. every thread takes the maximum of its share of the logits (16-byte
-//     loads); tau = the 32nd largest of these 1024 maxima, by a two-round
-//     radix select on 16-bit order keys (so at least 32 elements are >= tau);
-//  2. the elements >= tau (a few dozen on real logits) are gathered in LDS
-//     (16-byte groups whose maximum, kept in LDS by step 1, is below tau are
-//     skipped); among them V (exact) and the bigs follow by counting, and each
-//     big's slot in its reference thread's list by counting the larger bigs of
-//     that thread (one wave when there are at most 64); equal bigs in one
-//     thread mark it "replay";
+//     loads, all in flight together) and keeps its groups' maxima; tau = the
+//     32nd largest of these 1024 maxima, by a two-round radix select on 16-bit
+//     order keys (so at least 32 elements are >= tau): LDS-atomic histograms,
+//     a DPP prefix scan over the bins;
+//  2. the elements >= tau (a few dozen on real logits) are gathered in LDS,
+//     only by threads whose maximum reaches tau and only from groups whose
+//     maximum does (f16 compares with tau's value); among them V (exact) and
+//     the bigs follow by counting, and each big's slot in its reference
+//     thread's list by counting the larger bigs of that thread (one wave when
+//     there are at most 64, comparing only bigs whose thread holds two or
+//     more); equal bigs in one thread mark it "replay";
 //  3. the replayed threads run the reference heap, one wave per thread (heap
 //     in lanes 0..31, sifts by uniform readlanes), reading the logits again;
 //     more than kCap gathered elements (massive ties) replay all 256;
-//  4. the merge tree on the 256 lists in LDS, one merge per wave: list p in
-//     lanes 0..31, list p + s in lanes 32..63, the reversed compare one lane
-//     permute, the bitonic stages lane exchanges (DPP for strides 1-8) with
-//     the reference's strict compare-swap; merges whose second list is pure
-//     fill are skipped (lists are sorted descending, so they are no-ops).
+//  4. the merge tree on the 256 lists in LDS: list p in lanes 0..31, list
+//     p + s in lanes 32..63, the reversed compare and the stride-16 exchange
+//     by row swaps, strides 1-8 by DPP, with the reference's strict
+//     compare-swap. Merges whose second list is pure fill are skipped (lists
+//     are sorted descending, so they are no-ops); merges of two one-entry
+//     lists (or of an empty and a one-entry list) are closed-form; the rest
+//     run the network, two per wave side by side.
 #include <climits>
 
 #include "bp_device.hpp"

@@ -5,7 +5,7 @@
 // rows, softmax in f32, o = sum p_t v_t, f16 output. Two passes:
 //
 // Split pass (decode_split_kernel) — one workgroup per (group of KV heads,
-// range of `split_len` rows), the 1-D grid ordered XCD-aware. Each wave owns
+// range of `split_len` rows), the grid ordered XCD-aware. Each wave owns
 // one KV head (its 4 query heads) and streams 16-row batches with no
 // workgroup barrier in the main loop, the next batch loaded before the
 // current one is consumed (register double buffering). Loads are never
@@ -32,7 +32,9 @@
 //
 // Merge pass (decode_merge_kernel) — one 64-lane workgroup per (query head,
 // 32-dim chunk): log-sum-exp over the splits (attention_merge.wgsl:85-129),
-// every partial load issued up front.
+// every partial load issued up front, wave reductions by row swaps and DPP.
+// Its leading arguments are scalar kernel parameters, preloaded into SGPRs
+// at wave launch (this file is built with kernarg preloading).
 //
 // Fused step (launch_decode_step): the split pass also runs q_norm_rope on
 // the 4 query heads of its KV head (same code as the standalone kernel, so the

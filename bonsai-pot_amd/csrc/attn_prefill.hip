@@ -255,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
 
     const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);   // uniform: scalar registers
     const int lr = lane & 15, lg = lane >> 4;
     const bool is_b = (wave & 4) != 0;               // B wave (heavy tile) or A wave
     // Grid (KV head, head set, tile pair), KV head fastest: workgroups are

@@ -339,7 +339,7 @@ __device__ uint32_t select_key(TopKShared& sh, uint32_t key, uint32_t rank) {
 
 __global__ __launch_bounds__(kThreads) void topk_kernel(TopKArgs a) {
     __shared__ TopKShared sh;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint16_t* x = a.logits + (a.in_offset & ~1u);
     const uint32_t* words = reinterpret_cast<const uint32_t*>(x);
     const uint32_t n = a.n;

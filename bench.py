@@ -110,14 +110,20 @@ def time_region(torch, fn, steps, warmup):
     return start.elapsed_time(end) * 1e-3 / steps
 
 
-def per_launch_us(torch, b, launch, n_launch, replays=5):
+def per_launch_us(torch, b, launch, n_launch, replays=5, warm_s=0.03):
     """Average device time of one launch: n_launch launches (rotating layers) are
     captured in a HIP graph and replayed between two HIP events recorded on the
     stream the kernels run on, so host launch latency is excluded (inter-kernel
-    gaps of graph dispatch are included)."""
+    gaps of graph dispatch are included). The graph is first replayed for
+    warm_s seconds, so that the timed replays run at the clocks of sustained
+    load (a cold start measured up to 14 % slower)."""
     g = make_graph(torch, b, lambda: [launch(i) for i in range(n_launch)])
-    g.replay()
-    torch.cuda.synchronize()
+    t_end = time.perf_counter() + warm_s
+    while True:
+        g.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() >= t_end:
+            break
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -250,11 +256,28 @@ def bench_prefill(torch, args, m, pos):
     qn_us = per_launch_us(torch, b, lambda i: b.model.dispatch_q_norm_rope_fused(b.a, b.wp, b.q_off, 0, pos, m), n)
     wb_us = per_launch_us(torch, b, lambda i: b.model.dispatch_kv_writeback_fused(
         b.a, b.wp, b.k_off, b.v_off, b.cfg.head_dim, i % n_layer, pos, m), n)
+    # The fused step (bp_dispatch_attention_prefill_step: q norm + RoPE, K/V
+    # writeback and the attention kernel's f16 image in one preparation pass,
+    # then the attention kernel), its preparation pass alone, and the three
+    # separate dispatches it replaces.
+    args_step = (b.a, b.wp, b.q_off, b.k_off, b.v_off, b.out_off, 0, b.cfg.head_dim)
+    step_us = per_launch_us(torch, b, lambda i: b.model.dispatch_attention_prefill_step(
+        *args_step, i % n_layer, pos, m), n)
+    prep_us = per_launch_us(torch, b, lambda i: b.model.debug_prefill_prep(*args_step, i % n_layer, pos, m), n)
+
+    def _unfused(i):
+        b.model.dispatch_q_norm_rope_fused(b.a, b.wp, b.q_off, 0, pos, m)
+        b.model.dispatch_kv_writeback_fused(b.a, b.wp, b.k_off, b.v_off, b.cfg.head_dim, i % n_layer, pos, m)
+        b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True)
+    unfused_us = per_launch_us(torch, b, _unfused, n)
     b.model.close()
     return {"m_tokens": m, "pos_base": pos, "flops": flops, "kernel_us_avg": avg_us,
             "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS,
             "q_norm_rope_us": qn_us, "kv_writeback_us": wb_us,
-            "kv_writeback_GBps": m * 8 * (2 * 256 + 2 * 144) / (wb_us * 1e-6) / 1e9}
+            "kv_writeback_GBps": m * 8 * (2 * 256 + 2 * 144) / (wb_us * 1e-6) / 1e9,
+            "step_us": step_us, "step_prep_us": prep_us, "step_unfused_us": unfused_us,
+            "step_attention_us": step_us - prep_us,
+            "step_attention_frac_f16_mfma": flops / ((step_us - prep_us) * 1e-6) / 1e12 / F16_MFMA_PEAK_TFLOPS}
 
 
 def bench_copy(torch, args, nbytes=1 << 30):

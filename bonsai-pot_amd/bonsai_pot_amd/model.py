@@ -72,6 +72,8 @@ _SIGS = {
     "bp_dispatch_attention_decode_step": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
                                                   _u32]),
     "bp_dispatch_attention": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "bp_dispatch_attention_prefill_step": (_i32, [_vp, _vp, _vp] + [_u32] * 9),
+    "bp_debug_prefill_prep": (_i32, [_vp, _vp, _vp] + [_u32] * 9),
     "bp_dispatch_matvec_q1_0": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_matvec_q1_0_silu": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_matvec_q1_0_fused_normed": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
@@ -188,6 +190,22 @@ class Model:
                            m_tokens: int, is_prefill: bool) -> None:
         _check(lib.bp_dispatch_attention(self._h, act, q_off, out_off, layer_il, pos, m_tokens,
                                          1 if is_prefill else 0))
+
+    def dispatch_attention_prefill_step(self, act: int, w_norms: int, q_off: int, k_cur_off: int,
+                                        v_cur_off: int, out_off: int, w_q_norm_off: int,
+                                        w_k_norm_off: int, layer_il: int, pos: int,
+                                        m_tokens: int) -> None:
+        """q_norm_rope + kv_writeback + causal attention for m_tokens tokens, fused."""
+        _check(lib.bp_dispatch_attention_prefill_step(self._h, act, w_norms, q_off, k_cur_off,
+                                                      v_cur_off, out_off, w_q_norm_off,
+                                                      w_k_norm_off, layer_il, pos, m_tokens))
+
+    def debug_prefill_prep(self, act: int, w_norms: int, q_off: int, k_cur_off: int, v_cur_off: int,
+                           out_off: int, w_q_norm_off: int, w_k_norm_off: int, layer_il: int, pos: int,
+                           m_tokens: int) -> None:
+        """Measurement aid: the first launch of dispatch_attention_prefill_step alone."""
+        _check(lib.bp_debug_prefill_prep(self._h, act, w_norms, q_off, k_cur_off, v_cur_off, out_off,
+                                         w_q_norm_off, w_k_norm_off, layer_il, pos, m_tokens))
 
     # -- Q1_0 decode matvecs (src/forward.rs:212-334) -----------------------------
     # `weights` and `act` are device pointers (ints); w_d / w_qs byte offsets.

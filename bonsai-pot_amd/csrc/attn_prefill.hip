@@ -45,6 +45,7 @@
 //   D[i][j]: lane holds D[4g .. 4g+3][l % 16]
 #include "bp_device.hpp"
 #include "bp_kernels.hpp"
+#include "bp_norm_rope.hpp"
 
 namespace bp {
 namespace {
@@ -144,42 +145,22 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return static_cast<uint32_t>(f2h(a)) | (static_cast<uint32_t>(f2h(b)) << 16);
 }
 
-// Dequantization pass: one 256-thread workgroup per (64-row chunk, KV head)
-// writes the chunk's K rows (f16 and fp6 residual) and its V^T (dims x slots,
-// keys in v_slot order) to the image, zeros past n_rows. Each value is the
-// reference's f32 d * q; K keeps f16(k) plus 2^11 (k - f16(k)) in fp6 e2m3
-// with one power-of-two scale per 32-element block (the residual of a block:
-// 6 words of fp6, its E8M0 scale exponent less 11 in word 6, word 7 zero), V
-// keeps f16(v).
-//  K: thread t -> row t >> 2, Q8_0 block t & 3 (32 dims: 64 + 32 bytes out).
-//  V: thread t -> rows 4 (t >> 4) .. +3, dims 8 (t & 15) .. +7; each dim's 4
-//     values are 4 consecutive V^T slots, one 8-byte LDS write.
-__global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
-    const int t = threadIdx.x;
-    // Grid (KV head, chunk), KV head fastest (as in prefill_kernel): head g's
-    // chunks are written on the XCD whose L2 serves head g in the attention pass.
-    const uint32_t g = blockIdx.x, c = blockIdx.y;
-    const uint32_t nb_row = a.kv_dim / kBlock;
-    const uint32_t last = a.n_rows - 1;
-    // ---- loads (unconditional, clamped rows; rows past n_rows get d = 0) ----
+// Image of one 64-row chunk (chunk c of KV head g) from its Q8_0 values,
+// per thread of a 256-thread workgroup:
+//  K: thread t -> row t >> 2, Q8_0 block t & 3: kq0, kq1 its 32 bytes, kd its
+//     scale; writes 64 bytes of f16 and 32 bytes of residual;
+//  V: thread t -> rows 4 (t >> 4) .. +3, dims 8 (t & 15) .. +7: vq[i] the 8
+//     bytes of row 4 (t >> 4) + i, vd[i] its scale; each dim's 4 values are 4
+//     consecutive V^T slots, one 8-byte LDS write, then whole V^T rows out.
+// Each value is the reference's f32 d * q; K keeps f16(k) plus 2^11 (k -
+// f16(k)) in fp6 e2m3 with one power-of-two scale per 32-element block (the
+// residual of a block: 6 words of fp6, its E8M0 scale exponent less 11 in
+// word 6, word 7 zero), V keeps f16(v). Contains a workgroup barrier.
+__device__ __forceinline__ void emit_image_chunk(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const U4& kq0,
+                                                 const U4& kq1, float kd, const uint2 (&vq)[4], const float (&vd)[4],
+                                                 uint16_t (*vt)[kChunk + 8]) {
     const int kr = t >> 2, kb = t & 3;
-    const uint32_t krow = c * kChunk + kr, krc = min(krow, last);
-    const uint8_t* kqp = reinterpret_cast<const uint8_t*>(a.k.qs) + static_cast<uint64_t>(krc) * a.kv_dim + g * kHeadDim + 32 * kb;
-    const U4 kq0 = *reinterpret_cast<const U4*>(kqp), kq1 = *reinterpret_cast<const U4*>(kqp + 16);
-    float kd = a.k.d[static_cast<uint64_t>(krc) * nb_row + g * (kHeadDim / kBlock) + kb];
     const int vq4 = t >> 4, vdg = t & 15;
-    uint2 vq[4];
-    float vd[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t row = c * kChunk + 4 * vq4 + i, rc = min(row, last);
-        vq[i] = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.v.qs) +
-                                                static_cast<uint64_t>(rc) * a.kv_dim + g * kHeadDim + 8 * vdg);
-        vd[i] = a.v.d[static_cast<uint64_t>(rc) * nb_row + g * (kHeadDim / kBlock) + (vdg >> 2)];
-        if (row > last) vd[i] = 0.0f;
-    }
-    if (krow > last) kd = 0.0f;
     // ---- K rows: f16 value and fp6 residual of k = d * q (f32, as the
     // reference dequantizes) ----
     {
@@ -239,6 +220,222 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
         *reinterpret_cast<U4*>(vdst + v_addr(dim, (s0 >> 3) + i)) = *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
+}
+
+// The Q8_0 inputs of emit_image_chunk from the cache, for chunk c of KV head
+// g: unconditional loads of clamped rows; rows past n_rows get d = 0.
+__device__ __forceinline__ void load_chunk_q8(const PrefillArgs& a, uint32_t g, uint32_t c, int t, U4& kq0, U4& kq1,
+                                              float& kd, uint2 (&vq)[4], float (&vd)[4]) {
+    const uint32_t nb_row = a.kv_dim / kBlock;
+    const uint32_t last = a.n_rows - 1;
+    const int kr = t >> 2, kb = t & 3;
+    const uint32_t krow = c * kChunk + kr, krc = min(krow, last);
+    const uint8_t* kqp = reinterpret_cast<const uint8_t*>(a.k.qs) + static_cast<uint64_t>(krc) * a.kv_dim + g * kHeadDim + 32 * kb;
+    kq0 = *reinterpret_cast<const U4*>(kqp);
+    kq1 = *reinterpret_cast<const U4*>(kqp + 16);
+    kd = a.k.d[static_cast<uint64_t>(krc) * nb_row + g * (kHeadDim / kBlock) + kb];
+    const int vq4 = t >> 4, vdg = t & 15;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = c * kChunk + 4 * vq4 + i, rc = min(row, last);
+        vq[i] = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.v.qs) +
+                                                static_cast<uint64_t>(rc) * a.kv_dim + g * kHeadDim + 8 * vdg);
+        vd[i] = a.v.d[static_cast<uint64_t>(rc) * nb_row + g * (kHeadDim / kBlock) + (vdg >> 2)];
+        if (row > last) vd[i] = 0.0f;
+    }
+    if (krow > last) kd = 0.0f;
+}
+
+// Dequantization pass: one 256-thread workgroup per (64-row chunk, KV head)
+// writes the chunk's image from the cache, zeros past n_rows.
+__global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
+    const int t = threadIdx.x;
+    // Grid (KV head, chunk), KV head fastest (as in prefill_kernel): head g's
+    // chunks are written on the XCD whose L2 serves head g in the attention pass.
+    const uint32_t g = blockIdx.x, c = blockIdx.y;
+    U4 kq0, kq1;
+    float kd, vd[4];
+    uint2 vq[4];
+    load_chunk_q8(a, g, c, t, kq0, kq1, kd, vq, vd);
+    emit_image_chunk(a, g, c, t, kq0, kq1, kd, vq, vd, vt);
+}
+
+// Preparation pass of the fused prefill step (m_tokens new tokens at cache
+// rows [pos, pos + m_tokens)), in place of the dequantization pass. Grid (KV
+// head g, 64-row chunk c, part z), 256 threads:
+//  z = 0: kv_writeback (kv_writeback_fused.wgsl) of the chunk's new rows of
+//     KV head g into the cache, their Q8_0 bytes and scales also kept in LDS
+//     (the chunk's other rows are read from the cache, rows < pos, or are
+//     zero, rows past the last new row); then the chunk's image from those
+//     Q8_0 values (emit_image_chunk). Chunks with no new row run the
+//     dequantization pass's code.
+//  z = 1 .. 4: q_norm_rope (q_norm_rope_fused.wgsl) of query head 4 g + z - 1
+//     for the chunk's new tokens, in place.
+// Both use the 8-lane item form of the standalone kernels (bp_norm_rope.hpp),
+// so q, the cache bytes and the image are bit for bit those of q_norm_rope +
+// kv_writeback + the dequantization pass. Every offset is 8-element aligned
+// (the host checks it), so all item loads and stores are 16 bytes.
+__global__ __launch_bounds__(256, 4) void prefill_prep_kernel(PrefillArgs a, PrefillStepArgs w) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
+    __shared__ __attribute__((aligned(16))) uint8_t sq[2][kChunk][kHeadDim];   // K, V bytes of the chunk
+    __shared__ float sd[2][kChunk][kHeadDim / kBlock];                        // their scales
+    const int t = threadIdx.x;
+    const int lane = t & 63, L = lane & (kItemLanes - 1);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t g = blockIdx.x, c = blockIdx.y;
+    const uint32_t row0 = c * kChunk;
+    const uint32_t new_lo = max(row0, a.pos), new_hi = min(row0 + kChunk, a.pos + a.m_tokens);
+    U4 kq0, kq1;
+    float kd, vd[4];
+    uint2 vq[4];
+    if (new_lo >= new_hi) {   // rows before pos only
+        if (blockIdx.z > 0) return;
+        load_chunk_q8(a, g, c, t, kq0, kq1, kd, vq, vd);
+        emit_image_chunk(a, g, c, t, kq0, kq1, kd, vq, vd, vt);
+        return;
+    }
+    const uint32_t n_new = new_hi - new_lo, tok0 = new_lo - a.pos;
+    const uint32_t item = 8 * wave + (lane >> 3);   // this lane's item within a round of 32
+    constexpr int kRounds = kChunk / 32;             // rounds of 32 items cover the chunk's rows
+    if (blockIdx.z > 0) {
+        // ---- q_norm_rope of query head 4 g + z - 1 for the chunk's new tokens
+        // (item i: token tok0 + i), all loads first ----
+        const uint32_t head = g * kGroup + blockIdx.z - 1;
+        float wq0[8], wq1[8];
+        load8<true>(w.w_norms + w.w_q_off + 8 * L, wq0);
+        load8<true>(w.w_norms + w.w_q_off + 64 + 8 * L, wq1);
+        uint4 qx[kRounds][2], qcs[kRounds][2];
+        auto tok_of = [&](int r) { return tok0 + min(32u * r + item, n_new - 1); };   // dead items: a clamped one
+        auto q_ptr = [&](int r) { return w.q_act + static_cast<uint64_t>(tok_of(r)) * a.q_stride + head * kHeadDim; };
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            if (32u * r < n_new) {
+                const uint16_t* q = q_ptr(r);
+                qx[r][0] = *reinterpret_cast<const uint4*>(q + 8 * L);
+                qx[r][1] = *reinterpret_cast<const uint4*>(q + 64 + 8 * L);
+                const uint16_t* cs = w.rope_cs + static_cast<uint64_t>(a.pos + tok_of(r)) * kHeadDim + 16 * L;
+                qcs[r][0] = *reinterpret_cast<const uint4*>(cs);
+                qcs[r][1] = *reinterpret_cast<const uint4*>(cs + 8);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            if (32u * r < n_new) {
+                float x0[8], x1[8];
+                unpack8(qx[r][0], x0);
+                unpack8(qx[r][1], x1);
+                norm_rope8_vals(x0, x1, wq0, wq1, qcs[r][0], qcs[r][1], w.eps);
+                if (32u * r + item < n_new) {
+                    uint16_t* q = q_ptr(r);
+                    store8<true>(q + 8 * L, x0);   // q_norm_rope_fused.wgsl:95
+                    store8<true>(q + 64 + 8 * L, x1);
+                }
+            }
+        }
+        return;
+    }
+    const uint32_t nb_row = a.kv_dim / kBlock;
+    // Every load is issued before the arithmetic that needs it: the chunk's
+    // other rows, the weights, the new rows' K/V and table rows.
+    // ---- loads: rows of the chunk that are not new (thread t -> row t >> 2, block t & 3) ----
+    const uint32_t orr = t >> 2, okb = t & 3, orow = row0 + orr;
+    const bool other = orow < new_lo || orow >= new_hi;
+    uint4 ok0 = make_uint4(0, 0, 0, 0), ok1 = ok0, ov0 = ok0, ov1 = ok0;
+    float odk = 0.0f, odv = 0.0f;
+    if (other && orow < a.pos) {
+        const uint64_t qo = static_cast<uint64_t>(orow) * a.kv_dim + g * kHeadDim + 32 * okb;
+        const uint64_t dof = static_cast<uint64_t>(orow) * nb_row + g * (kHeadDim / kBlock) + okb;
+        ok0 = *reinterpret_cast<const uint4*>(a.k.qs + qo);
+        ok1 = *reinterpret_cast<const uint4*>(a.k.qs + qo + 16);
+        ov0 = *reinterpret_cast<const uint4*>(a.v.qs + qo);
+        ov1 = *reinterpret_cast<const uint4*>(a.v.qs + qo + 16);
+        odk = a.k.d[dof];
+        odv = a.v.d[dof];
+    }
+    // ---- loads: weights (dims 8L.., 64 + 8L..) ----
+    float wk0[8], wk1[8];
+    load8<true>(w.w_norms + w.w_k_off + 8 * L, wk0);
+    load8<true>(w.w_norms + w.w_k_off + 64 + 8 * L, wk1);
+    // ---- loads: new rows (item i: row new_lo + i), 2 rounds of 32 ----
+    constexpr int kKvRounds = kRounds;
+    uint4 kx[kKvRounds][2], vx[kKvRounds][2], kcs[kKvRounds][2];
+#pragma unroll
+    for (int r = 0; r < kKvRounds; r++) {
+        if (32u * r < n_new) {
+            const uint32_t row = new_lo + min(32u * r + item, n_new - 1), tok = row - a.pos;
+            const uint64_t tok_off = static_cast<uint64_t>(tok) * a.kv_dim + g * kHeadDim;
+            kx[r][0] = *reinterpret_cast<const uint4*>(w.k_cur + tok_off + 8 * L);
+            kx[r][1] = *reinterpret_cast<const uint4*>(w.k_cur + tok_off + 64 + 8 * L);
+            vx[r][0] = *reinterpret_cast<const uint4*>(w.v_cur + tok_off + 8 * L);
+            vx[r][1] = *reinterpret_cast<const uint4*>(w.v_cur + tok_off + 64 + 8 * L);
+            const uint16_t* cs = w.rope_cs + static_cast<uint64_t>(row) * kHeadDim + 16 * L;
+            kcs[r][0] = *reinterpret_cast<const uint4*>(cs);
+            kcs[r][1] = *reinterpret_cast<const uint4*>(cs + 8);
+        }
+    }
+    // ---- kv_writeback of the new rows: cache and LDS ----
+#pragma unroll
+    for (int r = 0; r < kKvRounds; r++) {
+        if (32u * r < n_new) {
+            float k0[8], k1[8], v0[8], v1[8];
+            unpack8(kx[r][0], k0);
+            unpack8(kx[r][1], k1);
+            unpack8(vx[r][0], v0);
+            unpack8(vx[r][1], v1);
+            norm_rope8_vals(k0, k1, wk0, wk1, kcs[r][0], kcs[r][1], w.eps);
+            uint2 pk0, pk1, pv0, pv1;
+            const float dk0 = quantize8(k0, pk0), dk1 = quantize8(k1, pk1);
+            const float dv0 = quantize8(v0, pv0), dv1 = quantize8(v1, pv1);
+            if (32u * r + item < n_new) {
+                const uint32_t rr = 32u * r + item + (new_lo - row0), row = row0 + rr;
+                const uint64_t qs_idx = static_cast<uint64_t>(row) * a.kv_dim + g * kHeadDim;
+                const uint64_t d_idx = static_cast<uint64_t>(row) * nb_row + g * (kHeadDim / kBlock);
+                *reinterpret_cast<uint2*>(w.k_qs + qs_idx + 8 * L) = pk0;
+                *reinterpret_cast<uint2*>(w.k_qs + qs_idx + 64 + 8 * L) = pk1;
+                *reinterpret_cast<uint2*>(w.v_qs + qs_idx + 8 * L) = pv0;
+                *reinterpret_cast<uint2*>(w.v_qs + qs_idx + 64 + 8 * L) = pv1;
+                *reinterpret_cast<uint2*>(&sq[0][rr][8 * L]) = pk0;
+                *reinterpret_cast<uint2*>(&sq[0][rr][64 + 8 * L]) = pk1;
+                *reinterpret_cast<uint2*>(&sq[1][rr][8 * L]) = pv0;
+                *reinterpret_cast<uint2*>(&sq[1][rr][64 + 8 * L]) = pv1;
+                if ((L & 3) == 0) {
+                    w.k_d[d_idx + (L >> 2)] = dk0;
+                    w.k_d[d_idx + 2 + (L >> 2)] = dk1;
+                    w.v_d[d_idx + (L >> 2)] = dv0;
+                    w.v_d[d_idx + 2 + (L >> 2)] = dv1;
+                    sd[0][rr][L >> 2] = dk0;
+                    sd[0][rr][2 + (L >> 2)] = dk1;
+                    sd[1][rr][L >> 2] = dv0;
+                    sd[1][rr][2 + (L >> 2)] = dv1;
+                }
+            }
+        }
+    }
+    // ---- the chunk's other rows into LDS (zero past the new rows) ----
+    if (other) {
+        *reinterpret_cast<uint4*>(&sq[0][orr][32 * okb]) = ok0;
+        *reinterpret_cast<uint4*>(&sq[0][orr][32 * okb + 16]) = ok1;
+        *reinterpret_cast<uint4*>(&sq[1][orr][32 * okb]) = ov0;
+        *reinterpret_cast<uint4*>(&sq[1][orr][32 * okb + 16]) = ov1;
+        sd[0][orr][okb] = odk;
+        sd[1][orr][okb] = odv;
+    }
+    __syncthreads();
+    // ---- 3. the image, from the chunk's Q8_0 values in LDS ----
+    {
+        const int kr = t >> 2, kb = t & 3;
+        kq0 = *reinterpret_cast<const U4*>(&sq[0][kr][32 * kb]);
+        kq1 = *reinterpret_cast<const U4*>(&sq[0][kr][32 * kb + 16]);
+        kd = sd[0][kr][kb];
+        const int vq4 = t >> 4, vdg = t & 15;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            vq[i] = *reinterpret_cast<const uint2*>(&sq[1][4 * vq4 + i][8 * vdg]);
+            vd[i] = sd[1][4 * vq4 + i][vdg >> 2];
+        }
+    }
+    emit_image_chunk(a, g, c, t, kq0, kq1, kd, vq, vd, vt);
 }
 
 // kHpw query heads per wave: 2 (a workgroup covers all 4 heads of its KV
@@ -575,13 +772,25 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
 }  // namespace
 
-hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(kv_dequant_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk), dim3(256), 0, s, a);
+static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
     if (a.heads_per_wave == 1)
         hipLaunchKernelGGL(prefill_kernel<1>, dim3(n_kv_head, 2, n_pairs), dim3(kThreads), 0, s, a);
     else
         hipLaunchKernelGGL(prefill_kernel<2>, dim3(n_kv_head, 1, n_pairs), dim3(kThreads), 0, s, a);
+}
+
+hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
+    hipLaunchKernelGGL(kv_dequant_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk), dim3(256), 0, s, a);
+    launch_attention(a, n_kv_head, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_step(const PrefillArgs& a, const PrefillStepArgs& w, uint32_t n_kv_head, hipStream_t s,
+                               bool prep_only) {
+    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk, 1 + kGroup), dim3(256), 0,
+                       s, a, w);
+    if (!prep_only) launch_attention(a, n_kv_head, s);
     return hipGetLastError();
 }
 

@@ -476,10 +476,11 @@ bp_status bp_dispatch_attention_decode_step(bp_model* m, void* act, const void* 
     return hip_check(m, bp::launch_decode_step(a, m->cfg.n_kv_head, m->stream), "attention_decode_step launch");
 }
 
-bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t out_off, uint32_t layer_il,
-                                uint32_t pos, uint32_t m_tokens, uint32_t is_prefill) {
-    bp_status st = enter(m);
-    if (st != BP_OK) return st;
+// Validates a batched-attention call (src/forward.rs:501-532) and fills its
+// PrefillArgs; BP_OK with a.m_tokens == 0 means there is nothing to do.
+static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t out_off, uint32_t layer_il,
+                              uint32_t pos, uint32_t m_tokens, uint32_t is_prefill, bp::PrefillArgs& a) {
+    a.m_tokens = 0;
     if (!act) return fail(BP_ERR_INVALID_ARG, "act is NULL");
     if (layer_il >= m->cfg.n_layer)
         return fail(BP_ERR_INVALID_ARG, "layer %u >= n_layer %u", layer_il, m->cfg.n_layer);
@@ -491,7 +492,6 @@ bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t
         return fail(BP_ERR_CONTEXT_OVERFLOW, "context overflow: pos %u + tokens %u > max_seq %u", pos,
                     m_tokens, m->max_seq);
     if (rows == 0) return fail(BP_ERR_INVALID_ARG, "attention over zero cache rows (pos 0, is_prefill 0)");
-    bp::PrefillArgs a;
     a.q = static_cast<const uint16_t*>(act) + q_off;
     a.out = static_cast<uint16_t*>(act) + out_off;
     a.k = kv_view(m, m->kv_k, layer_il);
@@ -518,7 +518,73 @@ bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t
     a.vt16 = m->kv16 + image_elems;
     a.kl8 = reinterpret_cast<uint8_t*>(m->kv16 + 2 * image_elems);
     a.n_rows = static_cast<uint32_t>(rows);
+    return BP_OK;
+}
+
+bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t out_off, uint32_t layer_il,
+                                uint32_t pos, uint32_t m_tokens, uint32_t is_prefill) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    bp::PrefillArgs a;
+    if ((st = prefill_args(m, act, q_off, out_off, layer_il, pos, m_tokens, is_prefill, a)) != BP_OK ||
+        a.m_tokens == 0)
+        return st;
     return hip_check(m, bp::launch_prefill(a, m->cfg.n_kv_head, m->stream), "attention launch");
+}
+
+// The fused prefill step, or (prep_only, a measurement aid) its first launch.
+static bp_status prefill_step(bp_model* m, void* act, const void* w_norms, uint32_t q_off, uint32_t k_cur_off,
+                              uint32_t v_cur_off, uint32_t out_off, uint32_t w_q_norm_off, uint32_t w_k_norm_off,
+                              uint32_t layer_il, uint32_t pos, uint32_t m_tokens, bool prep_only) {
+    bp_status st = enter(m);
+    if (st != BP_OK) return st;
+    if (!act || !w_norms) return fail(BP_ERR_INVALID_ARG, "act/w_norms is NULL");
+    bp::PrefillArgs a;
+    if ((st = prefill_args(m, act, q_off, out_off, layer_il, pos, m_tokens, 1, a)) != BP_OK || a.m_tokens == 0)
+        return st;
+    // The preparation pass moves 16-byte vectors only; other offsets take the
+    // three separate dispatches (same results).
+    const bool vec = ((k_cur_off | v_cur_off | w_q_norm_off | w_k_norm_off) & 7u) == 0 &&
+                     (reinterpret_cast<uintptr_t>(act) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w_norms) & 15u) == 0;
+    if (!vec && prep_only)
+        return fail(BP_ERR_INVALID_ARG, "prefill_prep: offsets must be multiples of 8, act/w_norms 16-byte aligned");
+    if (!vec) {
+        if ((st = bp_dispatch_q_norm_rope_fused(m, act, w_norms, q_off, w_q_norm_off, pos, m_tokens)) != BP_OK ||
+            (st = bp_dispatch_kv_writeback_fused(m, act, w_norms, k_cur_off, v_cur_off, w_k_norm_off, layer_il, pos,
+                                                 m_tokens)) != BP_OK)
+            return st;
+        return bp_dispatch_attention(m, act, q_off, out_off, layer_il, pos, m_tokens, 1);
+    }
+    bp::PrefillStepArgs w;
+    w.q_act = static_cast<uint16_t*>(act) + q_off;
+    w.k_cur = static_cast<const uint16_t*>(act) + k_cur_off;
+    w.v_cur = static_cast<const uint16_t*>(act) + v_cur_off;
+    w.w_norms = static_cast<const uint16_t*>(w_norms);
+    w.rope_cs = m->rope_cs;
+    w.w_q_off = w_q_norm_off;
+    w.w_k_off = w_k_norm_off;
+    w.k_d = const_cast<float*>(a.k.d);
+    w.k_qs = const_cast<int8_t*>(a.k.qs);
+    w.v_d = const_cast<float*>(a.v.d);
+    w.v_qs = const_cast<int8_t*>(a.v.qs);
+    w.eps = m->cfg.rms_eps;
+    return hip_check(m, bp::launch_prefill_step(a, w, m->cfg.n_kv_head, m->stream, prep_only),
+                     "attention_prefill_step launch");
+}
+
+bp_status bp_dispatch_attention_prefill_step(bp_model* m, void* act, const void* w_norms, uint32_t q_off,
+                                             uint32_t k_cur_off, uint32_t v_cur_off, uint32_t out_off,
+                                             uint32_t w_q_norm_off, uint32_t w_k_norm_off, uint32_t layer_il,
+                                             uint32_t pos, uint32_t m_tokens) {
+    return prefill_step(m, act, w_norms, q_off, k_cur_off, v_cur_off, out_off, w_q_norm_off, w_k_norm_off, layer_il,
+                        pos, m_tokens, false);
+}
+
+bp_status bp_debug_prefill_prep(bp_model* m, void* act, const void* w_norms, uint32_t q_off, uint32_t k_cur_off,
+                                uint32_t v_cur_off, uint32_t out_off, uint32_t w_q_norm_off, uint32_t w_k_norm_off,
+                                uint32_t layer_il, uint32_t pos, uint32_t m_tokens) {
+    return prefill_step(m, act, w_norms, q_off, k_cur_off, v_cur_off, out_off, w_q_norm_off, w_k_norm_off, layer_il,
+                        pos, m_tokens, true);
 }
 
 static bp_status matvec_common(bp_model* m, const void* weights, void* act, uint32_t k,

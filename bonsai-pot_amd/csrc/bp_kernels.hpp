@@ -105,6 +105,23 @@ struct PrefillArgs {
     uint32_t ws_chunks;       // 64-row chunks per KV head in the image
     uint32_t n_rows;          // rows the queries attend: cur of the last token
 };
+// Fused prefill step (q_norm_rope + kv_writeback + attention for the
+// m_tokens tokens at cache rows [pos, pos + m_tokens)): what the preparation
+// pass reads and writes besides PrefillArgs. All act / w_norms offsets are
+// multiples of 8 elements and the bases 16-byte aligned.
+struct PrefillStepArgs {
+    uint16_t* q_act;          // act + q_off: [m][n_head][128], normalized in place
+    const uint16_t* k_cur;    // act + k_cur_off: [m][kv_dim]
+    const uint16_t* v_cur;    // act + v_cur_off
+    const uint16_t* w_norms;
+    const uint16_t* rope_cs;  // [max_seq][64][(cos, sin)]
+    uint64_t w_q_off, w_k_off;
+    float* k_d;               // writable layer bases of the cache (the KvViews of PrefillArgs)
+    int8_t* k_qs;
+    float* v_d;
+    int8_t* v_qs;
+    float eps;
+};
 // Bytes of the K/V image for max_seq rows (one layer): f16 K, f16 V^T and
 // the K residual, 640 bytes per (row, KV head).
 inline uint64_t prefill_image_bytes(uint32_t n_kv_head, uint32_t max_seq) {
@@ -179,5 +196,9 @@ hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s)
 // Fused decode step: split pass (with q norm + row writeback) + merge pass.
 hipError_t launch_decode_step(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s);
+// The fused prefill step: preparation pass (in place of the dequantization
+// pass) and attention, 2 launches; with prep_only the first launch alone.
+hipError_t launch_prefill_step(const PrefillArgs& a, const PrefillStepArgs& w, uint32_t n_kv_head, hipStream_t s,
+                               bool prep_only);
 
 }  // namespace bp

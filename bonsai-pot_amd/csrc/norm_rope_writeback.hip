@@ -2,7 +2,7 @@
 //
 // Restates src/shaders/q_norm_rope_fused.wgsl and
 // src/shaders/kv_writeback_fused.wgsl (reference repository). Layout: 8 lanes
-// per (token, head) item, 8 items per wavefront (see kItemLanes below); the
+// per (token, head) item, 8 items per wavefront (kItemLanes, bp_norm_rope.hpp); the
 // fused decode step keeps the one-wave-per-item form of bp_norm_rope.hpp.
 //
 // Bit-exactness. Every f32 operation is one IEEE-rounded op in the order of
@@ -16,97 +16,6 @@
 
 namespace bp {
 namespace {
-
-// Standalone kernels: 8 lanes per (token, head) item, 8 items per wave, 4 waves
-// per workgroup. Lane L of an item holds dims 8L .. 8L+7 and their RoPE
-// partners 64 + 8L .. 64 + 8L+7, so loads and stores are 16-byte vectors and
-// the per-item scalar work (sqrt, the Q8_0 divides) is shared by 8 lanes
-// instead of 64. The RMSNorm sum reproduces the pairing tree of the 64-lane
-// butterfly exactly: partner j ^ 32 / 16 / 8 is lane L ^ 4 / 2 / 1 at the same
-// slot i, partner j ^ 4 / 2 / 1 is slot i ^ 4 / 2 / 1 of the same lane. Each
-// Q8_0 block is 4 lanes (block L / 4 for dims 8L.., 2 + L / 4 for 64 + 8L..).
-constexpr int kItemLanes = 8;
-
-template <bool kVec>
-__device__ __forceinline__ void load8(const uint16_t* p, float* out) {
-    if constexpr (kVec) {
-        const uint4 w = *reinterpret_cast<const uint4*>(p);
-        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            out[2 * i] = h2f(static_cast<uint16_t>(u[i]));
-            out[2 * i + 1] = h2f(static_cast<uint16_t>(u[i] >> 16));
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) out[i] = h2f(p[i]);
-    }
-}
-
-template <bool kVec>
-__device__ __forceinline__ void store8(uint16_t* p, const float* v) {
-    if constexpr (kVec) {
-        uint32_t u[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) u[i] = static_cast<uint32_t>(f2h(v[2 * i])) | (static_cast<uint32_t>(f2h(v[2 * i + 1])) << 16);
-        *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) p[i] = f2h(v[i]);
-    }
-}
-
-// RMSNorm * w + NEOX RoPE of one item in the 8-lane layout (same operations
-// as norm_rope_pair, per slot i): x0 = dims 8L + i, x1 = dims 64 + 8L + i.
-template <bool kVec>
-__device__ __forceinline__ void norm_rope8(float* x0, float* x1, const uint16_t* w, const uint16_t* cs_row,
-                                           int L, float eps) {
-    float s[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) s[i] = x0[i] * x0[i] + x1[i] * x1[i];
-#pragma unroll
-    for (int i = 0; i < 8; i++) s[i] = s[i] + lane_xor<4>(s[i]);   // j ^ 32
-#pragma unroll
-    for (int i = 0; i < 8; i++) s[i] = s[i] + lane_xor<2>(s[i]);   // j ^ 16
-#pragma unroll
-    for (int i = 0; i < 8; i++) s[i] = s[i] + lane_xor<1>(s[i]);   // j ^ 8
-    const float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];   // j ^ 4
-    const float sq = (t0 + t2) + (t1 + t3);                                                 // j ^ 2, j ^ 1
-    const float inv_h = 1.0f / sqrtf(sq / 128.0f + eps);
-    float w0[8], w1[8];
-    load8<kVec>(w + 8 * L, w0);
-    load8<kVec>(w + 64 + 8 * L, w1);
-    // cos/sin of pairs 8L .. 8L+7: 16 consecutive f16 of the table row.
-    const uint4 c0 = *reinterpret_cast<const uint4*>(cs_row + 16 * L);
-    const uint4 c1 = *reinterpret_cast<const uint4*>(cs_row + 16 * L + 8);
-    const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float c = h2f(static_cast<uint16_t>(cw[i])), sn = h2f(static_cast<uint16_t>(cw[i] >> 16));
-        const float n0 = x0[i] * inv_h * w0[i];
-        const float n1 = x1[i] * inv_h * w1[i];
-        x0[i] = n0 * c - n1 * sn;   // kv_writeback_fused.wgsl:102
-        x1[i] = n0 * sn + n1 * c;   // kv_writeback_fused.wgsl:107
-    }
-}
-
-// Q8_0 of the 8 values of one lane and its block (kv_writeback_fused.wgsl:118-200).
-__device__ __forceinline__ float quantize8(const float* x, uint2& packed) {
-    float a = fabsf(x[0]);
-#pragma unroll
-    for (int i = 1; i < 8; i++) a = fmaxf(a, fabsf(x[i]));
-    a = fmaxf(a, lane_xor<1>(a));
-    a = fmaxf(a, lane_xor<2>(a));
-    const float d = a / 127.0f;
-    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-    uint32_t b[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-        b[i] = static_cast<uint32_t>(static_cast<int>(fminf(fmaxf(rintf(x[i] * inv), -127.0f), 127.0f))) & 0xffu;
-    packed.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    packed.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-    return d;
-}
 
 __device__ __forceinline__ void quantize_store8(const float* x0, const float* x1, int L, float* d_row, int8_t* qs_row) {
     uint2 p0, p1;

@@ -12,6 +12,7 @@
  *                                       src/forward.rs:820-857
  *   bp_dispatch_attention_decode_step <- the three above for one token (fused, 2 launches)
  *   bp_dispatch_attention            <- dispatch_attention           src/forward.rs:501-532
+ *   bp_dispatch_attention_prefill_step <- q_norm_rope + kv_writeback + attention for m tokens (fused, 2 launches)
  *   bp_dispatch_matvec_q1_0          <- dispatch_matvec_q1_0         src/forward.rs:212-241
  *   bp_dispatch_matvec_q1_0_silu     <- dispatch_matvec_q1_0_silu    src/forward.rs:243-282
  *   bp_dispatch_matvec_q1_0_fused_normed <- dispatch_matvec_q1_0_fused_normed
@@ -147,6 +148,24 @@ bp_status bp_dispatch_attention(bp_model* model, void* act, uint32_t q_off, uint
                                 uint32_t layer_il, uint32_t pos, uint32_t m_tokens,
                                 uint32_t is_prefill);
 
+/* One whole causal prefill-attention step for one layer: m_tokens tokens at
+ * cache rows [pos, pos+m_tokens), in two launches instead of four, with the
+ * same results as
+ *   bp_dispatch_q_norm_rope_fused(act, w_norms, q_off, w_q_norm_off, pos, m_tokens)
+ *   bp_dispatch_kv_writeback_fused(act, w_norms, k_cur_off, v_cur_off, w_k_norm_off, layer_il, pos, m_tokens)
+ *   bp_dispatch_attention(act, q_off, out_off, layer_il, pos, m_tokens, 1)
+ * i.e. src/forward.rs:392-413 + :359-388 + :501-532 (the prefill layer's
+ * attention block, src/forward.rs:1075-1253). act[q_off] holds the raw
+ * queries and receives the normalized ones; cache rows [pos, pos+m_tokens)
+ * receive the new K/V; act[out_off] receives the attention output. q_off and
+ * out_off must be multiples of 8; when the other offsets are not (or act /
+ * w_norms are not 16-byte aligned) the call runs the three dispatches above. */
+bp_status bp_dispatch_attention_prefill_step(bp_model* model, void* act, const void* w_norms,
+                                             uint32_t q_off, uint32_t k_cur_off, uint32_t v_cur_off,
+                                             uint32_t out_off, uint32_t w_q_norm_off,
+                                             uint32_t w_k_norm_off, uint32_t layer_il, uint32_t pos,
+                                             uint32_t m_tokens);
+
 /* Q1_0 decode matvec family (src/shaders/matvec_q1_0*.wgsl). `weights` is the
  * device weight buffer; w_d / w_qs are BYTE offsets of a Q1_0 tensor in it
  * (d: n x (k/128) f16, then qs: n x (k/128) x 16 bytes, 4-byte aligned,
@@ -249,6 +268,16 @@ bp_status bp_attention_decode_noalloc(const bp_config* cfg, void* kv_k, void* kv
  * on `stream`. bench.py times it as the streaming-read floor of a decode's
  * byte count. */
 bp_status bp_debug_read_floor(const void* src, uint64_t bytes, void* sink, uint32_t n_workgroups, void* stream);
+
+/* Measurement aid, no counterpart in the reference: the first of the two
+ * launches of bp_dispatch_attention_prefill_step alone (q norm + RoPE, the
+ * K/V writeback and the attention kernel's f16 image of the layer's rows),
+ * same arguments; every act / w_norms offset must be a multiple of 8.
+ * bench.py times it to split the step's time between its two kernels. */
+bp_status bp_debug_prefill_prep(bp_model* model, void* act, const void* w_norms, uint32_t q_off,
+                                uint32_t k_cur_off, uint32_t v_cur_off, uint32_t out_off,
+                                uint32_t w_q_norm_off, uint32_t w_k_norm_off, uint32_t layer_il,
+                                uint32_t pos, uint32_t m_tokens);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* bp_last_error(void);

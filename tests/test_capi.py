@@ -90,6 +90,8 @@ def test_null_model_is_invalid_arg():
     assert bp.lib.bp_check_device(None) == errors.BP_ERR_INVALID_ARG
     assert b"NULL" in bp.lib.bp_last_error()
     assert bp.lib.bp_dispatch_attention(None, None, 0, 0, 0, 0, 1, 1) == errors.BP_ERR_INVALID_ARG
+    assert bp.lib.bp_dispatch_attention_prefill_step(None, None, None, 0, 0, 0, 0, 0, 0, 0, 0, 1) == \
+        errors.BP_ERR_INVALID_ARG
 
 
 # ---- KvSnapshot blob (src/kv_snapshot.rs:376-521) ----------------------------------

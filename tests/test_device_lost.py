@@ -62,6 +62,8 @@ def test_device_lost_latch_and_recovery(cuda):
         "bp_dispatch_attention_decode_step": lambda: L.bp_dispatch_attention_decode_step(
             h, a, w, 0, 0, 0, 0, 0, 128, 0, 8),
         "bp_dispatch_attention": lambda: L.bp_dispatch_attention(h, a, 0, 0, 0, 0, 4, 1),
+        "bp_dispatch_attention_prefill_step": lambda: L.bp_dispatch_attention_prefill_step(
+            h, a, w, 0, 0, 0, 0, 0, 128, 0, 0, 4),
         "bp_dispatch_matvec_q1_0": lambda: L.bp_dispatch_matvec_q1_0(h, s, a, 128, 16, 0, 64, 0, 128, 0),
         "bp_dispatch_matvec_q1_0_silu": lambda: L.bp_dispatch_matvec_q1_0_silu(h, s, a, 128, 16, 0, 64, 0, 128, 256, 0),
         "bp_dispatch_matvec_q1_0_fused_normed": lambda: L.bp_dispatch_matvec_q1_0_fused_normed(

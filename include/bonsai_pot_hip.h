@@ -154,8 +154,8 @@ bp_status bp_dispatch_attention(bp_model* model, void* act, uint32_t q_off, uint
  *   bp_dispatch_q_norm_rope_fused(act, w_norms, q_off, w_q_norm_off, pos, m_tokens)
  *   bp_dispatch_kv_writeback_fused(act, w_norms, k_cur_off, v_cur_off, w_k_norm_off, layer_il, pos, m_tokens)
  *   bp_dispatch_attention(act, q_off, out_off, layer_il, pos, m_tokens, 1)
- * i.e. src/forward.rs:392-413 + :359-388 + :501-532 (the prefill layer's
- * attention block, src/forward.rs:1075-1253). act[q_off] holds the raw
+ * i.e. src/forward.rs:392-413 + :359-388 + :501-532 as the prefill layer
+ * calls them (src/forward.rs:1141-1172). act[q_off] holds the raw
  * queries and receives the normalized ones; cache rows [pos, pos+m_tokens)
  * receive the new K/V; act[out_off] receives the attention output. q_off and
  * out_off must be multiples of 8; when the other offsets are not (or act /

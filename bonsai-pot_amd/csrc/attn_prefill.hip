@@ -145,76 +145,73 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return static_cast<uint32_t>(f2h(a)) | (static_cast<uint32_t>(f2h(b)) << 16);
 }
 
-// Image of one 64-row chunk (chunk c of KV head g) from its Q8_0 values,
-// per thread of a 256-thread workgroup:
-//  K: thread t -> row t >> 2, Q8_0 block t & 3: kq0, kq1 its 32 bytes, kd its
-//     scale; writes 64 bytes of f16 and 32 bytes of residual;
-//  V: thread t -> rows 4 (t >> 4) .. +3, dims 8 (t & 15) .. +7: vq[i] the 8
-//     bytes of row 4 (t >> 4) + i, vd[i] its scale; each dim's 4 values are 4
-//     consecutive V^T slots, one 8-byte LDS write, then whole V^T rows out.
+// Image of one 64-row chunk (chunk c of KV head g) from its Q8_0 values, in
+// three parts, each run by 256 threads (index t):
+//  emit_k_rows: thread t -> row t >> 2, Q8_0 block t & 3 (kq0, kq1 its 32
+//     bytes, kd its scale); writes 64 bytes of f16 and 32 bytes of residual;
+//  emit_v_lds: thread t -> rows 4 (t >> 4) .. +3, dims 8 (t & 15) .. +7 (vq[i]
+//     the 8 bytes of row 4 (t >> 4) + i, vd[i] its scale); each dim's 4 values
+//     are 4 consecutive V^T slots, one 8-byte write into the LDS tile vt;
+//  emit_v_rows (after a barrier): thread t -> V^T dim t >> 1, slots 32 (t & 1)
+//     .. +32 from vt to the image.
 // Each value is the reference's f32 d * q; K keeps f16(k) plus 2^11 (k -
 // f16(k)) in fp6 e2m3 with one power-of-two scale per 32-element block (the
 // residual of a block: 6 words of fp6, its E8M0 scale exponent less 11 in
-// word 6, word 7 zero), V keeps f16(v). Contains a workgroup barrier.
-__device__ __forceinline__ void emit_image_chunk(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const U4& kq0,
-                                                 const U4& kq1, float kd, const uint2 (&vq)[4], const float (&vd)[4],
-                                                 uint16_t (*vt)[kChunk + 8]) {
+// word 6, word 7 zero), V keeps f16(v).
+typedef uint16_t VTile[kHeadDim][kChunk + 8];
+__device__ __forceinline__ void emit_k_rows(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const U4& kq0,
+                                            const U4& kq1, float kd) {
     const int kr = t >> 2, kb = t & 3;
+    uint32_t w[16];
+    float r[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t x = i < 4 ? kq0.w[i] : kq1.w[i - 4];
+        float k[4];
+        _Float16 h[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            k[e] = kd * static_cast<float>(static_cast<int8_t>(x >> (8 * e)));
+            h[e] = static_cast<_Float16>(k[e]);
+            r[4 * i + e] = (k[e] - static_cast<float>(h[e])) * static_cast<float>(1 << kResidShift);
+            amax = fmaxf(amax, fabsf(r[4 * i + e]));
+        }
+        w[2 * i] = __builtin_bit_cast(uint32_t, f16x2{h[0], h[1]});
+        w[2 * i + 1] = __builtin_bit_cast(uint32_t, f16x2{h[2], h[3]});
+    }
+    // block scale 2^e, applied by the MFMA as E8M0 e + 127 - 11 (>= 0)
+    const int e = fp6_scale_exp(amax, kResidShift - kE8M0Bias);
+    const i32x6 p6 = pack32_fp6(r, e);
+    const uint32_t lo[8] = {static_cast<uint32_t>(p6[0]), static_cast<uint32_t>(p6[1]), static_cast<uint32_t>(p6[2]),
+                            static_cast<uint32_t>(p6[3]), static_cast<uint32_t>(p6[4]), static_cast<uint32_t>(p6[5]),
+                            static_cast<uint32_t>(e + kE8M0Bias - kResidShift), 0u};
+    uint16_t* kdst = a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        *reinterpret_cast<U4*>(kdst + k_addr(kr, 4 * kb + i)) = U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
+    uint8_t* ldst = a.kl8 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kLBytes;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        *reinterpret_cast<U4*>(ldst + l_addr(kr, 2 * kb + i)) = U4{{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]}};
+}
+__device__ __forceinline__ void emit_v_lds(int t, const uint2 (&vq)[4], const float (&vd)[4], VTile& vt) {
     const int vq4 = t >> 4, vdg = t & 15;
-    // ---- K rows: f16 value and fp6 residual of k = d * q (f32, as the
-    // reference dequantizes) ----
-    {
-        uint32_t w[16];
-        float r[32];
-        float amax = 0.0f;
+    const int slot = v_slot(4 * vq4);   // rows 4 vq4 .. +3 -> slots slot .. slot + 3
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t x = i < 4 ? kq0.w[i] : kq1.w[i - 4];
-            float k[4];
-            _Float16 h[4];
+    for (int e = 0; e < 8; e++) {   // dim 8 vdg + e
+        uint16_t hv[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                k[e] = kd * static_cast<float>(static_cast<int8_t>(x >> (8 * e)));
-                h[e] = static_cast<_Float16>(k[e]);
-                r[4 * i + e] = (k[e] - static_cast<float>(h[e])) * static_cast<float>(1 << kResidShift);
-                amax = fmaxf(amax, fabsf(r[4 * i + e]));
-            }
-            w[2 * i] = __builtin_bit_cast(uint32_t, f16x2{h[0], h[1]});
-            w[2 * i + 1] = __builtin_bit_cast(uint32_t, f16x2{h[2], h[3]});
+        for (int i = 0; i < 4; i++) {
+            const uint32_t word = e < 4 ? vq[i].x : vq[i].y;
+            const float v = vd[i] * static_cast<float>(static_cast<int8_t>(word >> (8 * (e & 3))));
+            hv[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
         }
-        // block scale 2^e, applied by the MFMA as E8M0 e + 127 - 11 (>= 0)
-        const int e = fp6_scale_exp(amax, kResidShift - kE8M0Bias);
-        const i32x6 p6 = pack32_fp6(r, e);
-        const uint32_t lo[8] = {static_cast<uint32_t>(p6[0]), static_cast<uint32_t>(p6[1]), static_cast<uint32_t>(p6[2]),
-                                static_cast<uint32_t>(p6[3]), static_cast<uint32_t>(p6[4]), static_cast<uint32_t>(p6[5]),
-                                static_cast<uint32_t>(e + kE8M0Bias - kResidShift), 0u};
-        uint16_t* kdst = a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            *reinterpret_cast<U4*>(kdst + k_addr(kr, 4 * kb + i)) = U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
-        uint8_t* ldst = a.kl8 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kLBytes;
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            *reinterpret_cast<U4*>(ldst + l_addr(kr, 2 * kb + i)) = U4{{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]}};
+        *reinterpret_cast<uint2*>(&vt[8 * vdg + e][slot]) =
+            make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16), hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
     }
-    // ---- V^T through LDS: f16(d * q) ----
-    {
-        const int slot = v_slot(4 * vq4);   // rows 4 vq4 .. +3 -> slots slot .. slot + 3
-#pragma unroll
-        for (int e = 0; e < 8; e++) {   // dim 8 vdg + e
-            uint16_t hv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t word = e < 4 ? vq[i].x : vq[i].y;
-                const float v = vd[i] * static_cast<float>(static_cast<int8_t>(word >> (8 * (e & 3))));
-                hv[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
-            }
-            *reinterpret_cast<uint2*>(&vt[8 * vdg + e][slot]) =
-                make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16), hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
-        }
-    }
-    __syncthreads();
-    // V^T rows: thread t -> dim t >> 1, slots 32 (t & 1) .. +32.
+}
+__device__ __forceinline__ void emit_v_rows(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const VTile& vt) {
     const int dim = t >> 1, s0 = 32 * (t & 1);
     uint16_t* vdst = a.vt16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kVHalves;
 #pragma unroll
@@ -222,10 +219,11 @@ __device__ __forceinline__ void emit_image_chunk(const PrefillArgs& a, uint32_t 
         *reinterpret_cast<U4*>(vdst + v_addr(dim, (s0 >> 3) + i)) = *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
 }
 
-// The Q8_0 inputs of emit_image_chunk from the cache, for chunk c of KV head
-// g: unconditional loads of clamped rows; rows past n_rows get d = 0.
-__device__ __forceinline__ void load_chunk_q8(const PrefillArgs& a, uint32_t g, uint32_t c, int t, U4& kq0, U4& kq1,
-                                              float& kd, uint2 (&vq)[4], float (&vd)[4]) {
+// The Q8_0 inputs of emit_k_rows / emit_v_lds from the cache, for chunk c of
+// KV head g and thread t (0..255): unconditional loads of clamped rows; rows
+// past n_rows get d = 0.
+__device__ __forceinline__ void load_k_q8(const PrefillArgs& a, uint32_t g, uint32_t c, int t, U4& kq0, U4& kq1,
+                                          float& kd) {
     const uint32_t nb_row = a.kv_dim / kBlock;
     const uint32_t last = a.n_rows - 1;
     const int kr = t >> 2, kb = t & 3;
@@ -234,6 +232,12 @@ __device__ __forceinline__ void load_chunk_q8(const PrefillArgs& a, uint32_t g, 
     kq0 = *reinterpret_cast<const U4*>(kqp);
     kq1 = *reinterpret_cast<const U4*>(kqp + 16);
     kd = a.k.d[static_cast<uint64_t>(krc) * nb_row + g * (kHeadDim / kBlock) + kb];
+    if (krow > last) kd = 0.0f;
+}
+__device__ __forceinline__ void load_v_q8(const PrefillArgs& a, uint32_t g, uint32_t c, int t, uint2 (&vq)[4],
+                                          float (&vd)[4]) {
+    const uint32_t nb_row = a.kv_dim / kBlock;
+    const uint32_t last = a.n_rows - 1;
     const int vq4 = t >> 4, vdg = t & 15;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -243,13 +247,12 @@ __device__ __forceinline__ void load_chunk_q8(const PrefillArgs& a, uint32_t g, 
         vd[i] = a.v.d[static_cast<uint64_t>(rc) * nb_row + g * (kHeadDim / kBlock) + (vdg >> 2)];
         if (row > last) vd[i] = 0.0f;
     }
-    if (krow > last) kd = 0.0f;
 }
 
 // Dequantization pass: one 256-thread workgroup per (64-row chunk, KV head)
 // writes the chunk's image from the cache, zeros past n_rows.
 __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
+    __shared__ __attribute__((aligned(16))) VTile vt;
     const int t = threadIdx.x;
     // Grid (KV head, chunk), KV head fastest (as in prefill_kernel): head g's
     // chunks are written on the XCD whose L2 serves head g in the attention pass.
@@ -257,27 +260,34 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
     U4 kq0, kq1;
     float kd, vd[4];
     uint2 vq[4];
-    load_chunk_q8(a, g, c, t, kq0, kq1, kd, vq, vd);
-    emit_image_chunk(a, g, c, t, kq0, kq1, kd, vq, vd, vt);
+    load_k_q8(a, g, c, t, kq0, kq1, kd);
+    load_v_q8(a, g, c, t, vq, vd);
+    emit_k_rows(a, g, c, t, kq0, kq1, kd);
+    emit_v_lds(t, vq, vd, vt);
+    __syncthreads();
+    emit_v_rows(a, g, c, t, vt);
 }
 
 // Preparation pass of the fused prefill step (m_tokens new tokens at cache
 // rows [pos, pos + m_tokens)), in place of the dequantization pass. Grid (KV
-// head g, 64-row chunk c, part z), 256 threads:
+// head g, 64-row chunk c, part z), 512 threads:
 //  z = 0: kv_writeback (kv_writeback_fused.wgsl) of the chunk's new rows of
 //     KV head g into the cache, their Q8_0 bytes and scales also kept in LDS
 //     (the chunk's other rows are read from the cache, rows < pos, or are
 //     zero, rows past the last new row); then the chunk's image from those
-//     Q8_0 values (emit_image_chunk). Chunks with no new row run the
-//     dequantization pass's code.
+//     Q8_0 values, K rows by threads 0-255 while threads 256-511 transpose V.
+//     Chunks with no new row take their Q8_0 values from the cache directly.
 //  z = 1 .. 4: q_norm_rope (q_norm_rope_fused.wgsl) of query head 4 g + z - 1
 //     for the chunk's new tokens, in place.
 // Both use the 8-lane item form of the standalone kernels (bp_norm_rope.hpp),
-// so q, the cache bytes and the image are bit for bit those of q_norm_rope +
-// kv_writeback + the dequantization pass. Every offset is 8-element aligned
-// (the host checks it), so all item loads and stores are 16 bytes.
-__global__ __launch_bounds__(256, 4) void prefill_prep_kernel(PrefillArgs a, PrefillStepArgs w) {
-    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];
+// one item per 8 lanes (64 items: every new row or token of the chunk at
+// once), so q, the cache bytes and the image are bit for bit those of
+// q_norm_rope + kv_writeback + the dequantization pass. Every offset is
+// 8-element aligned (the host checks it), so all item loads and stores are 16
+// bytes.
+constexpr int kPrepThreads = 512;
+__global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillArgs a, PrefillStepArgs w) {
+    __shared__ __attribute__((aligned(16))) VTile vt;
     __shared__ __attribute__((aligned(16))) uint8_t sq[2][kChunk][kHeadDim];   // K, V bytes of the chunk
     __shared__ float sd[2][kChunk][kHeadDim / kBlock];                        // their scales
     const int t = threadIdx.x;
@@ -286,156 +296,136 @@ __global__ __launch_bounds__(256, 4) void prefill_prep_kernel(PrefillArgs a, Pre
     const uint32_t g = blockIdx.x, c = blockIdx.y;
     const uint32_t row0 = c * kChunk;
     const uint32_t new_lo = max(row0, a.pos), new_hi = min(row0 + kChunk, a.pos + a.m_tokens);
+    const bool k_half = wave < 4;                      // threads 0-255: K rows; 256-511: V
+    const int th = t & 255;
     U4 kq0, kq1;
     float kd, vd[4];
     uint2 vq[4];
     if (new_lo >= new_hi) {   // rows before pos only
         if (blockIdx.z > 0) return;
-        load_chunk_q8(a, g, c, t, kq0, kq1, kd, vq, vd);
-        emit_image_chunk(a, g, c, t, kq0, kq1, kd, vq, vd, vt);
+        if (k_half) {
+            load_k_q8(a, g, c, th, kq0, kq1, kd);
+            emit_k_rows(a, g, c, th, kq0, kq1, kd);
+        } else {
+            load_v_q8(a, g, c, th, vq, vd);
+            emit_v_lds(th, vq, vd, vt);
+        }
+        __syncthreads();
+        if (!k_half) emit_v_rows(a, g, c, th, vt);
         return;
     }
     const uint32_t n_new = new_hi - new_lo, tok0 = new_lo - a.pos;
-    const uint32_t item = 8 * wave + (lane >> 3);   // this lane's item within a round of 32
-    constexpr int kRounds = kChunk / 32;             // rounds of 32 items cover the chunk's rows
+    const uint32_t item_raw = 8 * wave + (lane >> 3);   // this lane's item (0..63)
+    const bool live = item_raw < n_new;
+    const uint32_t item = live ? item_raw : n_new - 1;  // dead items compute on a clamped one
     if (blockIdx.z > 0) {
-        // ---- q_norm_rope of query head 4 g + z - 1 for the chunk's new tokens
-        // (item i: token tok0 + i), all loads first ----
-        const uint32_t head = g * kGroup + blockIdx.z - 1;
-        float wq0[8], wq1[8];
+        // ---- q_norm_rope of query head 4 g + z - 1, token tok0 + item ----
+        const uint32_t tok = tok0 + item;
+        uint16_t* q = w.q_act + static_cast<uint64_t>(tok) * a.q_stride + (g * kGroup + blockIdx.z - 1) * kHeadDim;
+        const uint4 qx0 = *reinterpret_cast<const uint4*>(q + 8 * L);
+        const uint4 qx1 = *reinterpret_cast<const uint4*>(q + 64 + 8 * L);
+        const uint16_t* cs = w.rope_cs + static_cast<uint64_t>(a.pos + tok) * kHeadDim + 16 * L;
+        const uint4 c0 = *reinterpret_cast<const uint4*>(cs), c1 = *reinterpret_cast<const uint4*>(cs + 8);
+        float wq0[8], wq1[8], x0[8], x1[8];
         load8<true>(w.w_norms + w.w_q_off + 8 * L, wq0);
         load8<true>(w.w_norms + w.w_q_off + 64 + 8 * L, wq1);
-        uint4 qx[kRounds][2], qcs[kRounds][2];
-        auto tok_of = [&](int r) { return tok0 + min(32u * r + item, n_new - 1); };   // dead items: a clamped one
-        auto q_ptr = [&](int r) { return w.q_act + static_cast<uint64_t>(tok_of(r)) * a.q_stride + head * kHeadDim; };
-#pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            if (32u * r < n_new) {
-                const uint16_t* q = q_ptr(r);
-                qx[r][0] = *reinterpret_cast<const uint4*>(q + 8 * L);
-                qx[r][1] = *reinterpret_cast<const uint4*>(q + 64 + 8 * L);
-                const uint16_t* cs = w.rope_cs + static_cast<uint64_t>(a.pos + tok_of(r)) * kHeadDim + 16 * L;
-                qcs[r][0] = *reinterpret_cast<const uint4*>(cs);
-                qcs[r][1] = *reinterpret_cast<const uint4*>(cs + 8);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            if (32u * r < n_new) {
-                float x0[8], x1[8];
-                unpack8(qx[r][0], x0);
-                unpack8(qx[r][1], x1);
-                norm_rope8_vals(x0, x1, wq0, wq1, qcs[r][0], qcs[r][1], w.eps);
-                if (32u * r + item < n_new) {
-                    uint16_t* q = q_ptr(r);
-                    store8<true>(q + 8 * L, x0);   // q_norm_rope_fused.wgsl:95
-                    store8<true>(q + 64 + 8 * L, x1);
-                }
-            }
+        unpack8(qx0, x0);
+        unpack8(qx1, x1);
+        norm_rope8_vals(x0, x1, wq0, wq1, c0, c1, w.eps);
+        if (live) {
+            store8<true>(q + 8 * L, x0);   // q_norm_rope_fused.wgsl:95
+            store8<true>(q + 64 + 8 * L, x1);
         }
         return;
     }
     const uint32_t nb_row = a.kv_dim / kBlock;
-    // Every load is issued before the arithmetic that needs it: the chunk's
-    // other rows, the weights, the new rows' K/V and table rows.
-    // ---- loads: rows of the chunk that are not new (thread t -> row t >> 2, block t & 3) ----
-    const uint32_t orr = t >> 2, okb = t & 3, orow = row0 + orr;
+    // ---- loads first: the chunk's other rows (thread t -> K or V, row
+    // (t & 255) >> 2, block t & 3), then the new row of this lane's item ----
+    const uint32_t orr = th >> 2, okb = th & 3, orow = row0 + orr;
     const bool other = orow < new_lo || orow >= new_hi;
-    uint4 ok0 = make_uint4(0, 0, 0, 0), ok1 = ok0, ov0 = ok0, ov1 = ok0;
-    float odk = 0.0f, odv = 0.0f;
+    uint4 o0 = make_uint4(0, 0, 0, 0), o1 = o0;
+    float od = 0.0f;
     if (other && orow < a.pos) {
+        const int8_t* qs = k_half ? a.k.qs : a.v.qs;
+        const float* dd = k_half ? a.k.d : a.v.d;
         const uint64_t qo = static_cast<uint64_t>(orow) * a.kv_dim + g * kHeadDim + 32 * okb;
-        const uint64_t dof = static_cast<uint64_t>(orow) * nb_row + g * (kHeadDim / kBlock) + okb;
-        ok0 = *reinterpret_cast<const uint4*>(a.k.qs + qo);
-        ok1 = *reinterpret_cast<const uint4*>(a.k.qs + qo + 16);
-        ov0 = *reinterpret_cast<const uint4*>(a.v.qs + qo);
-        ov1 = *reinterpret_cast<const uint4*>(a.v.qs + qo + 16);
-        odk = a.k.d[dof];
-        odv = a.v.d[dof];
+        o0 = *reinterpret_cast<const uint4*>(qs + qo);
+        o1 = *reinterpret_cast<const uint4*>(qs + qo + 16);
+        od = dd[static_cast<uint64_t>(orow) * nb_row + g * (kHeadDim / kBlock) + okb];
     }
-    // ---- loads: weights (dims 8L.., 64 + 8L..) ----
+    const uint32_t row = new_lo + item, tok = row - a.pos;
+    const uint64_t tok_off = static_cast<uint64_t>(tok) * a.kv_dim + g * kHeadDim;
+    const uint4 kx0 = *reinterpret_cast<const uint4*>(w.k_cur + tok_off + 8 * L);
+    const uint4 kx1 = *reinterpret_cast<const uint4*>(w.k_cur + tok_off + 64 + 8 * L);
+    const uint4 vx0 = *reinterpret_cast<const uint4*>(w.v_cur + tok_off + 8 * L);
+    const uint4 vx1 = *reinterpret_cast<const uint4*>(w.v_cur + tok_off + 64 + 8 * L);
+    const uint16_t* cs = w.rope_cs + static_cast<uint64_t>(row) * kHeadDim + 16 * L;
+    const uint4 c0 = *reinterpret_cast<const uint4*>(cs), c1 = *reinterpret_cast<const uint4*>(cs + 8);
     float wk0[8], wk1[8];
     load8<true>(w.w_norms + w.w_k_off + 8 * L, wk0);
     load8<true>(w.w_norms + w.w_k_off + 64 + 8 * L, wk1);
-    // ---- loads: new rows (item i: row new_lo + i), 2 rounds of 32 ----
-    constexpr int kKvRounds = kRounds;
-    uint4 kx[kKvRounds][2], vx[kKvRounds][2], kcs[kKvRounds][2];
-#pragma unroll
-    for (int r = 0; r < kKvRounds; r++) {
-        if (32u * r < n_new) {
-            const uint32_t row = new_lo + min(32u * r + item, n_new - 1), tok = row - a.pos;
-            const uint64_t tok_off = static_cast<uint64_t>(tok) * a.kv_dim + g * kHeadDim;
-            kx[r][0] = *reinterpret_cast<const uint4*>(w.k_cur + tok_off + 8 * L);
-            kx[r][1] = *reinterpret_cast<const uint4*>(w.k_cur + tok_off + 64 + 8 * L);
-            vx[r][0] = *reinterpret_cast<const uint4*>(w.v_cur + tok_off + 8 * L);
-            vx[r][1] = *reinterpret_cast<const uint4*>(w.v_cur + tok_off + 64 + 8 * L);
-            const uint16_t* cs = w.rope_cs + static_cast<uint64_t>(row) * kHeadDim + 16 * L;
-            kcs[r][0] = *reinterpret_cast<const uint4*>(cs);
-            kcs[r][1] = *reinterpret_cast<const uint4*>(cs + 8);
-        }
-    }
     // ---- kv_writeback of the new rows: cache and LDS ----
-#pragma unroll
-    for (int r = 0; r < kKvRounds; r++) {
-        if (32u * r < n_new) {
-            float k0[8], k1[8], v0[8], v1[8];
-            unpack8(kx[r][0], k0);
-            unpack8(kx[r][1], k1);
-            unpack8(vx[r][0], v0);
-            unpack8(vx[r][1], v1);
-            norm_rope8_vals(k0, k1, wk0, wk1, kcs[r][0], kcs[r][1], w.eps);
-            uint2 pk0, pk1, pv0, pv1;
-            const float dk0 = quantize8(k0, pk0), dk1 = quantize8(k1, pk1);
-            const float dv0 = quantize8(v0, pv0), dv1 = quantize8(v1, pv1);
-            if (32u * r + item < n_new) {
-                const uint32_t rr = 32u * r + item + (new_lo - row0), row = row0 + rr;
-                const uint64_t qs_idx = static_cast<uint64_t>(row) * a.kv_dim + g * kHeadDim;
-                const uint64_t d_idx = static_cast<uint64_t>(row) * nb_row + g * (kHeadDim / kBlock);
-                *reinterpret_cast<uint2*>(w.k_qs + qs_idx + 8 * L) = pk0;
-                *reinterpret_cast<uint2*>(w.k_qs + qs_idx + 64 + 8 * L) = pk1;
-                *reinterpret_cast<uint2*>(w.v_qs + qs_idx + 8 * L) = pv0;
-                *reinterpret_cast<uint2*>(w.v_qs + qs_idx + 64 + 8 * L) = pv1;
-                *reinterpret_cast<uint2*>(&sq[0][rr][8 * L]) = pk0;
-                *reinterpret_cast<uint2*>(&sq[0][rr][64 + 8 * L]) = pk1;
-                *reinterpret_cast<uint2*>(&sq[1][rr][8 * L]) = pv0;
-                *reinterpret_cast<uint2*>(&sq[1][rr][64 + 8 * L]) = pv1;
-                if ((L & 3) == 0) {
-                    w.k_d[d_idx + (L >> 2)] = dk0;
-                    w.k_d[d_idx + 2 + (L >> 2)] = dk1;
-                    w.v_d[d_idx + (L >> 2)] = dv0;
-                    w.v_d[d_idx + 2 + (L >> 2)] = dv1;
-                    sd[0][rr][L >> 2] = dk0;
-                    sd[0][rr][2 + (L >> 2)] = dk1;
-                    sd[1][rr][L >> 2] = dv0;
-                    sd[1][rr][2 + (L >> 2)] = dv1;
-                }
+    {
+        float k0[8], k1[8], v0[8], v1[8];
+        unpack8(kx0, k0);
+        unpack8(kx1, k1);
+        unpack8(vx0, v0);
+        unpack8(vx1, v1);
+        norm_rope8_vals(k0, k1, wk0, wk1, c0, c1, w.eps);
+        uint2 pk0, pk1, pv0, pv1;
+        const float dk0 = quantize8(k0, pk0), dk1 = quantize8(k1, pk1);
+        const float dv0 = quantize8(v0, pv0), dv1 = quantize8(v1, pv1);
+        if (live) {
+            const uint32_t rr = row - row0;
+            const uint64_t qs_idx = static_cast<uint64_t>(row) * a.kv_dim + g * kHeadDim;
+            const uint64_t d_idx = static_cast<uint64_t>(row) * nb_row + g * (kHeadDim / kBlock);
+            *reinterpret_cast<uint2*>(w.k_qs + qs_idx + 8 * L) = pk0;
+            *reinterpret_cast<uint2*>(w.k_qs + qs_idx + 64 + 8 * L) = pk1;
+            *reinterpret_cast<uint2*>(w.v_qs + qs_idx + 8 * L) = pv0;
+            *reinterpret_cast<uint2*>(w.v_qs + qs_idx + 64 + 8 * L) = pv1;
+            *reinterpret_cast<uint2*>(&sq[0][rr][8 * L]) = pk0;
+            *reinterpret_cast<uint2*>(&sq[0][rr][64 + 8 * L]) = pk1;
+            *reinterpret_cast<uint2*>(&sq[1][rr][8 * L]) = pv0;
+            *reinterpret_cast<uint2*>(&sq[1][rr][64 + 8 * L]) = pv1;
+            if ((L & 3) == 0) {
+                w.k_d[d_idx + (L >> 2)] = dk0;
+                w.k_d[d_idx + 2 + (L >> 2)] = dk1;
+                w.v_d[d_idx + (L >> 2)] = dv0;
+                w.v_d[d_idx + 2 + (L >> 2)] = dv1;
+                sd[0][rr][L >> 2] = dk0;
+                sd[0][rr][2 + (L >> 2)] = dk1;
+                sd[1][rr][L >> 2] = dv0;
+                sd[1][rr][2 + (L >> 2)] = dv1;
             }
         }
     }
     // ---- the chunk's other rows into LDS (zero past the new rows) ----
     if (other) {
-        *reinterpret_cast<uint4*>(&sq[0][orr][32 * okb]) = ok0;
-        *reinterpret_cast<uint4*>(&sq[0][orr][32 * okb + 16]) = ok1;
-        *reinterpret_cast<uint4*>(&sq[1][orr][32 * okb]) = ov0;
-        *reinterpret_cast<uint4*>(&sq[1][orr][32 * okb + 16]) = ov1;
-        sd[0][orr][okb] = odk;
-        sd[1][orr][okb] = odv;
+        const int kv = k_half ? 0 : 1;
+        *reinterpret_cast<uint4*>(&sq[kv][orr][32 * okb]) = o0;
+        *reinterpret_cast<uint4*>(&sq[kv][orr][32 * okb + 16]) = o1;
+        sd[kv][orr][okb] = od;
     }
     __syncthreads();
-    // ---- 3. the image, from the chunk's Q8_0 values in LDS ----
-    {
-        const int kr = t >> 2, kb = t & 3;
+    // ---- the image, from the chunk's Q8_0 values in LDS: K rows by threads
+    // 0-255, V^T by threads 256-511 ----
+    if (k_half) {
+        const int kr = th >> 2, kb = th & 3;
         kq0 = *reinterpret_cast<const U4*>(&sq[0][kr][32 * kb]);
         kq1 = *reinterpret_cast<const U4*>(&sq[0][kr][32 * kb + 16]);
         kd = sd[0][kr][kb];
-        const int vq4 = t >> 4, vdg = t & 15;
+        emit_k_rows(a, g, c, th, kq0, kq1, kd);
+    } else {
+        const int vq4 = th >> 4, vdg = th & 15;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             vq[i] = *reinterpret_cast<const uint2*>(&sq[1][4 * vq4 + i][8 * vdg]);
             vd[i] = sd[1][4 * vq4 + i][vdg >> 2];
         }
+        emit_v_lds(th, vq, vd, vt);
     }
-    emit_image_chunk(a, g, c, t, kq0, kq1, kd, vq, vd, vt);
+    __syncthreads();
+    if (!k_half) emit_v_rows(a, g, c, th, vt);
 }
 
 // kHpw query heads per wave: 2 (a workgroup covers all 4 heads of its KV
@@ -788,8 +778,8 @@ hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t 
 
 hipError_t launch_prefill_step(const PrefillArgs& a, const PrefillStepArgs& w, uint32_t n_kv_head, hipStream_t s,
                                bool prep_only) {
-    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk, 1 + kGroup), dim3(256), 0,
-                       s, a, w);
+    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk, 1 + kGroup),
+                       dim3(kPrepThreads), 0, s, a, w);
     if (!prep_only) launch_attention(a, n_kv_head, s);
     return hipGetLastError();
 }

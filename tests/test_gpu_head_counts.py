@@ -84,3 +84,27 @@ def test_prefill(cuda, monkeypatch, kv, m, pos_base, hpw):
     dev.attention(0, pos_base, is_prefill=True)
     want = sc.oracle_attention(0, pos_base, is_prefill=True)
     assert_attn_close(dev.out_f32(), want, f"prefill n_kv_head={kv} m={m} pos_base={pos_base}")
+
+
+@pytest.mark.parametrize("kv", KV_HEADS)
+@pytest.mark.parametrize("m,pos", [(70, 0), (33, 100)])
+def test_prefill_step(cuda, kv, m, pos):
+    """The fused prefill step (preparation pass over (KV head, chunk, part)
+    grids of this head count): cache bytes and normalized q bit-exact,
+    attention within tolerance."""
+    _say(f"[heads] prefill step n_kv_head={kv} m={m} pos={pos}")
+    cfg = _cfg(kv)
+    sc = Scenario(cfg, max_seq=pos + m + 3, m_tokens=m, seed=60 + kv + m + pos, w_std=0.1)
+    _prefill_cache(sc, 1, pos, seed=70 + kv + pos)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.model.dispatch_attention_prefill_step(dev.act.data_ptr(), dev.w.data_ptr(), sc.q_off, sc.k_off,
+                                              sc.v_off, sc.out_off, sc.w_q_off, sc.w_k_off, 1, pos, m)
+    sc.oracle_q_norm_rope(pos)
+    sc.oracle_writeback(1, pos)
+    k, v = dev.kv_host()
+    assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v), "cache bytes differ"
+    act = dev.act_host()
+    q = slice(sc.q_off, sc.q_off + m * cfg.q_dim)
+    assert np.array_equal(act[q], sc.act[q]), "normalized q differs"
+    want = sc.oracle_attention(1, pos, is_prefill=True)
+    assert_attn_close(dev.out_f32(), want, f"prefill step n_kv_head={kv} m={m} pos={pos}")

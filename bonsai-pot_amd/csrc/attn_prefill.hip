@@ -17,7 +17,9 @@
 //    (1-D grid, KV head fastest: one head per XCD). Wave w (SIMD w & 3) owns
 //    unit (w & 3) of tile A if w < 4, of tile B otherwise. For short prompts
 //    (fewer tile pairs x KV heads than CUs) a unit is 16 tokens x 1 head and
-//    two workgroups split the 4 query heads of a (KV head, pair).
+//    two workgroups split the 4 query heads of a (KV head, pair); for shorter
+//    ones four 4-wave workgroups (one query head each, wave w on unit w & 1 of
+//    tile A if w < 2, of tile B otherwise).
 //  * Work balance (split-K inside the workgroup): with n_A / n_B the 64-row
 //    chunks tiles A / B attend and mid = ceil((n_A + n_B) / 2), the B waves
 //    take B's chunks [0, mid) while the A waves take A's chunks [0, n_A) and
@@ -53,7 +55,6 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 512;
 constexpr int kChunk = 64;               // cache rows per LDS chunk
 constexpr int kSub = kChunk / 16;        // 16-row S^T sub-tiles per chunk
 constexpr int kKHalves = kChunk * kHeadDim;   // K rows, 256 B each
@@ -428,15 +429,17 @@ __global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillAr
     if (!k_half) emit_v_rows(a, g, c, th, vt);
 }
 
-// kHpw query heads per wave: 2 (a workgroup covers all 4 heads of its KV
-// head), or 1 for short prompts, where two workgroups (head sets) share a
-// (KV head, tile pair) and every wave does half the work, so that twice the
-// workgroups run.
-template <int kHpw>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+// Layouts (kHpw query heads per wave, kWaves waves per workgroup):
+//  <2, 8>: a workgroup covers all 4 heads of its KV head;
+//  <1, 8>: short prompts: two workgroups (head sets) share a (KV head, tile
+//      pair) and every wave does half the work, so that twice the workgroups run;
+//  <1, 4>: shorter prompts: four workgroups of 4 waves (one query head each)
+//      per (KV head, tile pair), one wave per SIMD.
+template <int kHpw, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
     constexpr int kHeadsPerWave = kHpw;
-    constexpr int kHeadSets = 2 / kHpw;   // the grid's y extent (query-head sets per KV head)
-    static_assert(kHeadSets * kHpw == 2, "two query heads per wave pair");
+    constexpr int kUnits = kWaves / 2;     // units per tile: (token half, head group)
+    static_assert((kWaves == 8 && (kHpw == 1 || kHpw == 2)) || (kWaves == 4 && kHpw == 1), "layout");
     // lds[stream][buf]: staged chunk (K rows, V^T rows, K residual rows), 2
     // streams x 2 buffers (160 KB, all of the CU's LDS).
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);   // uniform: scalar registers
     const int lr = lane & 15, lg = lane >> 4;
-    const bool is_b = (wave & 4) != 0;               // B wave (heavy tile) or A wave
+    const bool is_b = (wave & kUnits) != 0;          // B wave (heavy tile) or A wave
     // Grid (KV head, head set, tile pair), KV head fastest: workgroups are
     // dealt to the 8 XCDs round-robin by linear id (x fastest), so with 8 KV
     // heads each XCD serves one head and its L2 holds that head's K/V for all
@@ -452,7 +455,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     // divisions at the kernel's start.)
     const uint32_t g = blockIdx.x, hs = blockIdx.y, pair = blockIdx.z;
     const uint32_t tile_a = pair, tile_b = a.n_tiles - 1 - pair;   // tile_b >= tile_a
-    const uint32_t h0 = g * kGroup + 2 * hs + kHeadsPerWave * ((wave >> 1) & 1);   // first query head
+    const uint32_t h0 = kWaves == 4 ? g * kGroup + hs   // first query head
+                                    : g * kGroup + 2 * hs + kHeadsPerWave * ((wave >> 1) & 1);
     const uint32_t utok = 16 * (wave & 1);            // unit's first token within its tile
     const float c2 = a.scale * 1.4426950408889634f;   // scores in log2 units
 
@@ -547,8 +551,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
     // ---- staging: a chunk's K rows, V^T and K residual (40 KB, already
     // swizzled in the image) copied straight into LDS by global_load_lds (no
-    // registers): wave w's copy k (0..4) moves 1 KB, pieces 512 k + 64 w + lane
-    // (K: k = 0, 1; V^T: k = 2, 3; residual: k = 4). -------------------------------
+    // registers): each copy of a wave moves 1 KB, 16-byte pieces 64 (kWaves k +
+    // w) + lane of K (1024 pieces), V^T (1024) and the residual (512). ---------
     const uint16_t* k16 = a.k16 + static_cast<uint64_t>(g) * a.ws_chunks * kKHalves;
     const uint16_t* vt16 = a.vt16 + static_cast<uint64_t>(g) * a.ws_chunks * kVHalves;
     const uint8_t* kl8 = a.kl8 + static_cast<uint64_t>(g) * a.ws_chunks * kLBytes;
@@ -557,11 +561,14 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
         const uint16_t* ks = k16 + static_cast<uint64_t>(c) * kKHalves;
         const uint16_t* vs = vt16 + static_cast<uint64_t>(c) * kVHalves;
         const uint16_t* ls = reinterpret_cast<const uint16_t*>(kl8 + static_cast<uint64_t>(c) * kLBytes);
+        constexpr int kKv = 16 / kWaves, kRes = 8 / kWaves;   // copies per wave: K (and V^T), residual
 #pragma unroll
-        for (int k = 0; k < 5; k++) {
-            const int piece = 512 * (k & 1) + 64 * wv;   // 16-byte pieces within K, V^T or residual
-            const uint16_t* src = (k < 2 ? ks : k < 4 ? vs : ls) + 8 * ((k < 4 ? piece : 64 * wv) + lane);
-            uint16_t* dst = buf + (k < 2 ? 0 : k < 4 ? kKHalves : kKHalves + kVHalves) + 8 * (k < 4 ? piece : 64 * wv);
+        for (int k = 0; k < 2 * kKv + kRes; k++) {
+            const int sec = k < kKv ? 0 : k < 2 * kKv ? 1 : 2;   // K, V^T, residual
+            const int kk = sec == 0 ? k : sec == 1 ? k - kKv : k - 2 * kKv;
+            const int piece = 64 * (kWaves * kk + wv);           // 16-byte pieces within the section
+            const uint16_t* src = (sec == 0 ? ks : sec == 1 ? vs : ls) + 8 * (piece + lane);
+            uint16_t* dst = buf + (sec == 0 ? 0 : sec == 1 ? kKHalves : kKHalves + kVHalves) + 8 * piece;
             __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
                                              (void __attribute__((address_space(3)))*)dst, 16, 0, 0);
         }
@@ -722,9 +729,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
     // ---- merge the two halves of tile B: A waves hand (O, m, l) to B waves --
     // (the staging buffers are free: every wave is past the last barrier).
-    float* xo = reinterpret_cast<float*>(&lds[0][0][0]);   // [4 units][2 h][8 dt][4][64 lanes]
-    float* xml = xo + 4 * kHeadsPerWave * 8 * 4 * 64;      // [4 units][2 h][2][64 lanes]
-    const int unit = wave & 3;
+    float* xo = reinterpret_cast<float*>(&lds[0][0][0]);        // [kUnits][h][8 dt][4][64 lanes]
+    float* xml = xo + kUnits * kHeadsPerWave * 8 * 4 * 64;      // [kUnits][h][2][64 lanes]
+    const int unit = wave & (kUnits - 1);
     if (!is_b) {
 #pragma unroll
         for (int h = 0; h < kHeadsPerWave; h++) {
@@ -764,10 +771,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
 
 static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
-    if (a.heads_per_wave == 1)
-        hipLaunchKernelGGL(prefill_kernel<1>, dim3(n_kv_head, 2, n_pairs), dim3(kThreads), 0, s, a);
+    if (a.heads_per_wave == 2)
+        hipLaunchKernelGGL((prefill_kernel<2, 8>), dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
+    else if (a.wg_waves == 4)
+        hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4, n_pairs), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(prefill_kernel<2>, dim3(n_kv_head, 1, n_pairs), dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL((prefill_kernel<1, 8>), dim3(n_kv_head, 2, n_pairs), dim3(512), 0, s, a);
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {

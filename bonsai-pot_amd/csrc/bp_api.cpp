@@ -44,6 +44,7 @@ struct bp_model {
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
     uint32_t prefill_hpw;   // 0 = by grid size, else 1 or 2 query heads per prefill wave
+    uint32_t prefill_waves; // 0 = by grid size, else 4 or 8 waves per workgroup at 1 head per wave
     int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 (default) f16 sums in the reference's order, 2 i8 MFMA
     uint32_t matvec_stream_min_tiles;
     bool lost;
@@ -265,6 +266,11 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
     if (const char* env = std::getenv("BP_PREFILL_HEADS_PER_WAVE")) {
         const long v = std::strtol(env, nullptr, 10);
         if (v == 1 || v == 2) m->prefill_hpw = static_cast<uint32_t>(v);
+    }
+    m->prefill_waves = 0;
+    if (const char* env = std::getenv("BP_PREFILL_WG_WAVES")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v == 4 || v == 8) m->prefill_waves = static_cast<uint32_t>(v);
     }
     // Q1_0 matvec arithmetic. Default "f16": the reference's f16 block sums in
     // its order, bit for bit (VALU-bound), so logits and hence top-k token
@@ -506,10 +512,15 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
         // One query head per wave (twice the workgroups, half the work each) while
         // that grid still fits the compute units at one workgroup each; measured
         // at 128-1024 tokens 1.3-1.4x faster, at 1536 (384 workgroups) 1.25x
-        // slower. BP_PREFILL_HEADS_PER_WAVE forces either layout.
+        // slower. Then 4-wave workgroups (four times the workgroups of the
+        // two-heads layout) while those fit. BP_PREFILL_HEADS_PER_WAVE and
+        // BP_PREFILL_WG_WAVES force a layout.
         const uint32_t pairs = (a.n_tiles + 1) / 2;
         const uint32_t cus = static_cast<uint32_t>(m->cu_count > 0 ? m->cu_count : 256);
         a.heads_per_wave = m->prefill_hpw != 0 ? m->prefill_hpw : (2 * pairs * m->cfg.n_kv_head <= cus ? 1u : 2u);
+        a.wg_waves = 8;
+        if (a.heads_per_wave == 1)
+            a.wg_waves = m->prefill_waves != 0 ? m->prefill_waves : (4 * pairs * m->cfg.n_kv_head <= cus ? 4u : 8u);
     }
     a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:524
     a.ws_chunks = (m->max_seq + 63) / 64;

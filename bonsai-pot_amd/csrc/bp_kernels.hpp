@@ -89,7 +89,8 @@ struct PrefillArgs {
     uint32_t pos;             // first query's RoPE/cache position when causal
     uint32_t causal;          // 1: token m sees rows [0, pos+m]; 0: rows [0, pos)
     uint32_t n_tiles;         // ceil(m_tokens / kPrefillTileTok)
-    uint32_t heads_per_wave;  // prefill_kernel layout: 2, or 1 (two workgroups per tile pair)
+    uint32_t heads_per_wave;  // prefill_kernel layout: 2, or 1 (two or four workgroups per tile pair)
+    uint32_t wg_waves;        // with 1 head per wave: 8 (two head sets) or 4 (four, one head each)
     float scale;
     // Image of the layer's K and V, written by the dequantization pass for
     // rows [0, n_rows) (zeros up to the next 64-row chunk), per KV head g:

@@ -71,9 +71,10 @@ def test_decode_step(cuda, kv, pos):
 
 @pytest.mark.parametrize("kv", KV_HEADS)
 @pytest.mark.parametrize("m,pos_base", [(70, 0), (33, 100)])
-@pytest.mark.parametrize("hpw", ["1", "2"])
+@pytest.mark.parametrize("hpw", ["1", "1w4", "2"])
 def test_prefill(cuda, monkeypatch, kv, m, pos_base, hpw):
-    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw)
+    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw[0])
+    monkeypatch.setenv("BP_PREFILL_WG_WAVES", "4" if hpw.endswith("w4") else "8")
     _say(f"[heads] prefill n_kv_head={kv} m={m} pos_base={pos_base} heads_per_wave={hpw}")
     cfg = _cfg(kv)
     sc = Scenario(cfg, max_seq=pos_base + m + 3, m_tokens=m, seed=40 + kv + m + pos_base)

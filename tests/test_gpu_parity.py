@@ -141,13 +141,15 @@ def test_decode_ctx32k_with_outlier_rows(cuda):
 
 @pytest.mark.parametrize("m,pos_base", [(1, 0), (17, 0), (64, 0), (65, 0), (100, 5), (512, 0),
                                         (130, 1000), (33, 31), (200, 900)])
-@pytest.mark.parametrize("hpw", ["1", "2"])
+@pytest.mark.parametrize("hpw", ["1", "1w4", "2"])
 def test_prefill_vs_oracle(cuda, monkeypatch, m, pos_base, hpw):
-    """Both prefill_kernel layouts (1 or 2 query heads per wave; by default the
-    grid size picks one), forced through BP_PREFILL_HEADS_PER_WAVE. (200, 900)
+    """Every prefill_kernel layout (1 query head per wave in 8- or 4-wave
+    workgroups, or 2 per wave; by default the grid size picks one), forced
+    through BP_PREFILL_HEADS_PER_WAVE and BP_PREFILL_WG_WAVES. (200, 900)
     gives second-half units whose first chunk lies wholly past some tokens'
     last row (all scores masked while the running max is still unset)."""
-    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw)
+    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw[0])
+    monkeypatch.setenv("BP_PREFILL_WG_WAVES", "4" if hpw.endswith("w4") else "8")
     _say(f"[prefill] m={m} pos_base={pos_base} heads_per_wave={hpw}")
     cfg = layout.Config(n_layer=2)
     sc = Scenario(cfg, max_seq=pos_base + m + 3, m_tokens=m, seed=300 + m + pos_base)
@@ -269,14 +271,15 @@ def test_fused_decode_step_sequence(cuda):
     assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v)
 
 
-@pytest.mark.parametrize("hpw", ["1", "2"])
+@pytest.mark.parametrize("hpw", ["1", "1w4", "2"])
 @pytest.mark.parametrize("m,pos_base", [(512, 0), (200, 900)])
 def test_prefill_with_outlier_key_rows(cuda, monkeypatch, m, pos_base, hpw):
     """Causal prefill over a cache whose K rows are 1 % x8 (rows of the chunk
     itself and of the cached prefix): scores far above the running max drive
     the lazy rescale with P up to 2^8 in f16. The cache [0, pos_base + m) is
     written by the oracle; the device runs the attention only."""
-    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw)
+    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw[0])
+    monkeypatch.setenv("BP_PREFILL_WG_WAVES", "4" if hpw.endswith("w4") else "8")
     _say(f"[prefill-outliers] m={m} pos_base={pos_base} heads_per_wave={hpw}")
     cfg = layout.Config(n_layer=2)
     sc = Scenario(cfg, max_seq=pos_base + m + 1, m_tokens=m, seed=1300 + m + pos_base)

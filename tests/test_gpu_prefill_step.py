@@ -70,11 +70,12 @@ def test_prefill_step_matches_separate_dispatches(cuda, m, pos):
     _same(dev_a, dev_b, f"m={m} pos={pos}")
 
 
-@pytest.mark.parametrize("hpw", ["1", "2"])
+@pytest.mark.parametrize("hpw", ["1", "1w4", "2"])
 @pytest.mark.parametrize("m,pos", [(17, 0), (100, 5), (200, 900)])
 def test_prefill_step_vs_oracle(cuda, monkeypatch, m, pos, hpw):
     """The fused step against the oracle directly, in both attention layouts."""
-    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw)
+    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", hpw[0])
+    monkeypatch.setenv("BP_PREFILL_WG_WAVES", "4" if hpw.endswith("w4") else "8")
     _say(f"[prefill-step] oracle m={m} pos={pos} heads_per_wave={hpw}")
     sc = _scenario(m, pos, seed=2000 + m + pos)
     dev = DeviceScenario(sc, upload_kv=True)

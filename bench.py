@@ -626,6 +626,8 @@ def main():
         extras["prefill_pp512"] = bench_prefill(torch, args, 512, 0)
     if args.only in (None, "chunked"):
         extras["chunked_prefill_2048_on_2048"] = bench_prefill(torch, args, 2048, 2048)
+        # a short chunk over a long cache (a chat turn): the key-split layout
+        extras["chunked_prefill_64_on_16384"] = bench_prefill(torch, args, 64, 16384)
     if args.only in (None, "matvec"):
         extras["matvec_q1_0_4b_layer"] = bench_matvec(torch, args)
     if args.only in (None, "matmul"):

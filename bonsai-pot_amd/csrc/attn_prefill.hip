@@ -67,6 +67,7 @@ constexpr int kBufHalves = kKHalves + kVHalves + kLBytes / 2;   // one staged ch
 constexpr int kResidShift = 11;
 constexpr int kE8M0Bias = 127;
 constexpr float kLazy = 8.0f;            // lazy-rescale threshold (log2 units)
+constexpr int kSplitStride = kHeadDim + 4;   // floats per key-split partial: O, m, l, 2 pad (16-byte rows)
 
 struct alignas(16) U4 { uint32_t w[4]; };
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -453,8 +454,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
     // heads each XCD serves one head and its L2 holds that head's K/V for all
     // the head's tile pairs. (Grid dimensions instead of a 1-D id: no integer
     // divisions at the kernel's start.)
-    const uint32_t g = blockIdx.x, hs = blockIdx.y, pair = blockIdx.z;
-    const uint32_t tile_a = pair, tile_b = a.n_tiles - 1 - pair;   // tile_b >= tile_a
+    // With a key split (a.n_ksplit > 1, 4-wave layout only) the grid is (KV
+    // head, split x 4 + head set, tile): each workgroup takes one tile
+    // (self-paired) and the key chunks [c_lo, c_lo + split_chunks) of it.
+    constexpr uint32_t kSets = kWaves == 4 ? 4 : 2 / kHpw;   // head sets per KV head
+    const bool ksplit = kWaves == 4 && a.n_ksplit > 1;
+    const uint32_t g = blockIdx.x, pair = blockIdx.z;
+    const uint32_t hs = ksplit ? blockIdx.y % kSets : blockIdx.y, ks = ksplit ? blockIdx.y / kSets : 0u;
+    const uint32_t tile_a = pair, tile_b = ksplit ? pair : a.n_tiles - 1 - pair;   // tile_b >= tile_a
     const uint32_t h0 = kWaves == 4 ? g * kGroup + hs   // first query head
                                     : g * kGroup + 2 * hs + kHeadsPerWave * ((wave >> 1) & 1);
     const uint32_t utok = 16 * (wave & 1);            // unit's first token within its tile
@@ -466,7 +473,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
         return a.causal ? a.pos + last + 1 : a.pos;
     };
     const uint32_t kend_b = tile_kend(tile_b);
-    const uint32_t n_b = (kend_b + kChunk - 1) / kChunk;
+    const uint32_t n_tot = (kend_b + kChunk - 1) / kChunk;   // chunks tile B attends
+    const uint32_t c_lo = ksplit ? min(ks * a.split_chunks, n_tot) : 0u;
+    const uint32_t n_b = ksplit ? min(a.split_chunks, n_tot - c_lo) : n_tot;   // this workgroup's share
     const uint32_t n_a = tile_b == tile_a ? 0u : (tile_kend(tile_a) + kChunk - 1) / kChunk;
     const uint32_t mid = (n_a + n_b + 1) / 2;        // B waves: [0, mid); A waves: [mid, n_b) of B
     const uint32_t n_iter = mid;                     // >= n_a + (n_b - mid)
@@ -696,13 +705,16 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
 
     // ---- main loop: iteration i computes stream-1 chunk i and (i >= n_a)
     // stream-2 chunk mid + i - n_a; loads for i+1 are issued first -----------
-    auto c1_of = [&](uint32_t i) { return i; };                      // valid while i < mid
+    auto c1_of = [&](uint32_t i) { return c_lo + i; };               // valid while i < mid
     auto has2 = [&](uint32_t i) { return i >= n_a && mid + (i - n_a) < n_b; };
-    auto c2_of = [&](uint32_t i) { return mid + (i - n_a); };
+    auto c2_of = [&](uint32_t i) { return c_lo + mid + (i - n_a); };
     // A copy into LDS completes when the issuing wave's vmcnt drains; the
-    // barrier after that wait publishes it to the workgroup.
-    load_chunk(lds[0][0], c1_of(0));
-    if (has2(0)) load_chunk(lds[1][0], c2_of(0));
+    // barrier after that wait publishes it to the workgroup. (A key split
+    // past the tile's last chunk has no iterations and copies nothing.)
+    if (n_iter > 0) {
+        load_chunk(lds[0][0], c1_of(0));
+        if (has2(0)) load_chunk(lds[1][0], c2_of(0));
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (uint32_t i = 0; i < n_iter; i++) {
@@ -746,9 +758,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
     __syncthreads();
     if (!is_b) return;
     const bool split = mid < n_b;   // the A waves computed B's chunks [mid, n_b)
+    float m_fin[kHeadsPerWave];
 #pragma unroll
     for (int h = 0; h < kHeadsPerWave; h++) {
         float mb = m_run[h], lb = l_acc[h][0];
+        m_fin[h] = mb;
         if (split) {
             const float ma = xml[((unit * kHeadsPerWave + h) * 2 + 0) * 64 + lane];
             const float la = xml[((unit * kHeadsPerWave + h) * 2 + 1) * 64 + lane];
@@ -761,10 +775,50 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
                 for (int j = 0; j < 4; j++)
                     o[h][dt][j] = o[h][dt][j] * eb + xo[(((unit * kHeadsPerWave + h) * 8 + dt) * 4 + j) * 64 + lane] * ea;
             lb = lb * eb + la * ea;
+            m_fin[h] = mm;
         }
         l_run[h] = lb;
     }
+    if (ksplit) {
+        // partial (O unnormalized, m in log2 units, l) of this key split
+        if (!unit_live || my_tok >= a.m_tokens) return;
+        const uint32_t n_head = a.q_stride / kHeadDim;
+#pragma unroll
+        for (int h = 0; h < kHeadsPerWave; h++) {
+            float* pp = a.kpart + ((static_cast<uint64_t>(my_tok) * n_head + h0 + h) * a.n_ksplit + ks) * kSplitStride;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+                *reinterpret_cast<f32x4*>(pp + 16 * dt + 4 * lg) = o[h][dt];
+            if (lg == 0) *reinterpret_cast<float2*>(pp + kHeadDim) = make_float2(m_fin[h], l_run[h]);
+        }
+        return;
+    }
     write_unit();
+}
+
+// Key-split merge: one wave per (token, query head); lane l combines dims
+// 2l, 2l + 1 of the n_ksplit partials by their log-sum-exp weights (as the
+// decode merge, attention_merge.wgsl:85-129) and stores f16(O / L).
+__global__ __launch_bounds__(64) void prefill_merge_kernel(PrefillArgs a) {
+    const int lane = threadIdx.x;
+    const uint32_t tok = blockIdx.x, h = blockIdx.y;
+    const uint32_t n_head = a.q_stride / kHeadDim, ns = a.n_ksplit;
+    const float* pp = a.kpart + (static_cast<uint64_t>(tok) * n_head + h) * ns * kSplitStride;
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, pp[s * kSplitStride + kHeadDim]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (uint32_t s = 0; s < ns; s++) {
+        const float* q = pp + s * kSplitStride;
+        const float ms = q[kHeadDim];
+        const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);   // splits without rows
+        L = __builtin_fmaf(w, q[kHeadDim + 1], L);
+        const float2 v = *reinterpret_cast<const float2*>(q + 2 * lane);
+        o0 = __builtin_fmaf(w, v.x, o0);
+        o1 = __builtin_fmaf(w, v.y, o1);
+    }
+    const float inv_l = 1.0f / L;
+    *reinterpret_cast<uint32_t*>(a.out + static_cast<uint64_t>(tok) * a.q_stride + h * kHeadDim + 2 * lane) =
+        pack2(o0 * inv_l, o1 * inv_l);
 }
 
 }  // namespace
@@ -773,7 +827,10 @@ static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
     if (a.heads_per_wave == 2)
         hipLaunchKernelGGL((prefill_kernel<2, 8>), dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
-    else if (a.wg_waves == 4)
+    else if (a.wg_waves == 4 && a.n_ksplit > 1) {
+        hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4 * a.n_ksplit, a.n_tiles), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.m_tokens, n_kv_head * kGroup), dim3(64), 0, s, a);
+    } else if (a.wg_waves == 4)
         hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4, n_pairs), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL((prefill_kernel<1, 8>), dim3(n_kv_head, 2, n_pairs), dim3(512), 0, s, a);

@@ -45,6 +45,7 @@ struct bp_model {
     uint32_t decode_wide_min_rows;
     uint32_t prefill_hpw;   // 0 = by grid size, else 1 or 2 query heads per prefill wave
     uint32_t prefill_waves; // 0 = by grid size, else 4 or 8 waves per workgroup at 1 head per wave
+    uint32_t prefill_ksplit;   // 0 = by grid size, else the key split count of the 4-wave layout
     int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 (default) f16 sums in the reference's order, 2 i8 MFMA
     uint32_t matvec_stream_min_tiles;
     bool lost;
@@ -97,6 +98,9 @@ bp_status check_model(const bp_model* m) {
 }
 
 // Makes the model's device current for this thread.
+// Floats per prefill key-split partial (O, m, l, 2 pad), as attn_prefill.hip.
+constexpr uint64_t kPrefillSplitStride = 132;
+
 bp_status enter(bp_model* m) {
     bp_status st = check_model(m);
     if (st != BP_OK) return st;
@@ -267,6 +271,11 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
         const long v = std::strtol(env, nullptr, 10);
         if (v == 1 || v == 2) m->prefill_hpw = static_cast<uint32_t>(v);
     }
+    m->prefill_ksplit = 0;
+    if (const char* env = std::getenv("BP_PREFILL_KSPLIT")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 1 && v <= 64) m->prefill_ksplit = static_cast<uint32_t>(v);
+    }
     m->prefill_waves = 0;
     if (const char* env = std::getenv("BP_PREFILL_WG_WAVES")) {
         const long v = std::strtol(env, nullptr, 10);
@@ -289,8 +298,12 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 1) m->matvec_stream_min_tiles = static_cast<uint32_t>(v);
     }
-    m->partials_floats = static_cast<uint64_t>(cfg->n_head) * bp::decode_max_splits() *
-                         bp::decode_partial_stride();
+    // Split-K partials, shared (stream order) by decode (n_head x its splits)
+    // and the prefill key split (token x split products up to
+    // kPrefillSplitTok, 132 floats each per query head).
+    m->partials_floats = std::max<uint64_t>(
+        static_cast<uint64_t>(cfg->n_head) * bp::decode_max_splits() * bp::decode_partial_stride(),
+        static_cast<uint64_t>(cfg->n_head) * bp::kPrefillSplitTok * kPrefillSplitStride);
     const size_t rope_elems = static_cast<size_t>(max_seq) * cfg->head_dim;
     if (hipMalloc(&m->kv_k, m->kv_bytes) != hipSuccess || hipMalloc(&m->kv_v, m->kv_bytes) != hipSuccess ||
         hipMalloc(&m->rope_cs, rope_elems * 2) != hipSuccess ||
@@ -521,6 +534,26 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
         a.wg_waves = 8;
         if (a.heads_per_wave == 1)
             a.wg_waves = m->prefill_waves != 0 ? m->prefill_waves : (4 * pairs * m->cfg.n_kv_head <= cus ? 4u : 8u);
+        // Key split for short chunks over long caches (4-wave layout): while
+        // one workgroup per (tile, KV head, query head) leaves most CUs idle,
+        // split every tile's key range over n_ksplit workgroups of at least 8
+        // chunks each (fewer splits when the partials would not fit), then
+        // merge. BP_PREFILL_KSPLIT forces a split count (within the partials).
+        a.n_ksplit = 1;
+        a.split_chunks = 0;
+        a.kpart = m->partials;
+        if (a.heads_per_wave == 1 && a.wg_waves == 4 && is_prefill) {
+            const uint32_t chunks = static_cast<uint32_t>((rows + 63) / 64);   // the last tile's key chunks
+            const uint32_t wgs = a.n_tiles * 4 * m->cfg.n_kv_head;           // workgroups per split
+            uint32_t ns = m->prefill_ksplit != 0 ? m->prefill_ksplit
+                                                  : std::min<uint32_t>(std::max<uint32_t>(cus / wgs, 1u), chunks / 8);
+            const uint64_t cap = m->partials_floats / (static_cast<uint64_t>(m->cfg.n_head) * kPrefillSplitStride);
+            while (ns > 1 && static_cast<uint64_t>(m_tokens) * ns > cap) --ns;
+            if (ns > 1) {
+                a.n_ksplit = ns;
+                a.split_chunks = (chunks + ns - 1) / ns;
+            }
+        }
     }
     a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:524
     a.ws_chunks = (m->max_seq + 63) / 64;

@@ -91,6 +91,14 @@ struct PrefillArgs {
     uint32_t n_tiles;         // ceil(m_tokens / kPrefillTileTok)
     uint32_t heads_per_wave;  // prefill_kernel layout: 2, or 1 (two or four workgroups per tile pair)
     uint32_t wg_waves;        // with 1 head per wave: 8 (two head sets) or 4 (four, one head each)
+    // Key split (short chunks over long caches): n_ksplit > 1 workgroups per
+    // (tile, KV head, head set), each over split_chunks 64-row chunks of the
+    // tile's key range, write partial (O, m, l) to kpart, [m][n_head][n_ksplit]
+    // x 132 floats (O, m, l, pad); prefill_merge_kernel combines them. 4-wave
+    // layout only.
+    uint32_t n_ksplit;
+    uint32_t split_chunks;
+    float* kpart;
     float scale;
     // Image of the layer's K and V, written by the dequantization pass for
     // rows [0, n_rows) (zeros up to the next 64-row chunk), per KV head g:
@@ -123,6 +131,9 @@ struct PrefillStepArgs {
     int8_t* v_qs;
     float eps;
 };
+// Token x split products the key-split partials are sized for (the host
+// picks n_ksplit within it).
+constexpr uint32_t kPrefillSplitTok = 512;
 // Bytes of the K/V image for max_seq rows (one layer): f16 K, f16 V^T and
 // the K residual, 640 bytes per (row, KV head).
 inline uint64_t prefill_image_bytes(uint32_t n_kv_head, uint32_t max_seq) {

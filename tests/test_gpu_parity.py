@@ -313,3 +313,30 @@ def test_config1_real_cache_last_layer(cuda):
     # and the plain decode entry point on the same cache
     dev.decode(35, pos)
     assert_attn_close(dev.out_f32(1)[0], want, "config1 layer 35 decode")
+
+
+@pytest.mark.parametrize("m,pos_base,ksplit", [(1, 4000, "auto"), (16, 3000, "auto"), (16, 3000, "3"),
+                                               (70, 2500, "auto"), (70, 2500, "7"), (100, 5, "4"),
+                                               (33, 31, "2"), (64, 640, "40")])
+def test_prefill_key_split(cuda, monkeypatch, m, pos_base, ksplit):
+    """Short chunks over long caches: the 4-wave layout splits every tile's key
+    range over several workgroups and merges their partials (forced split
+    counts include ones whose last splits lie past some tiles' keys, and one
+    above the chunk count)."""
+    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", "1")
+    monkeypatch.setenv("BP_PREFILL_WG_WAVES", "4")
+    if ksplit != "auto":
+        monkeypatch.setenv("BP_PREFILL_KSPLIT", ksplit)
+    _say(f"[prefill-ksplit] m={m} pos_base={pos_base} ksplit={ksplit}")
+    cfg = layout.Config(n_layer=2)
+    sc = Scenario(cfg, max_seq=pos_base + m + 3, m_tokens=m, seed=900 + m + pos_base)
+    if pos_base >= 100:   # 1 % of the cache's K rows x8 (the lazy-rescale stress)
+        write_outlier_rows(sc, 0, pos_base, seed=960 + m)
+    else:
+        _prefill_cache(sc, 0, pos_base, seed=950 + pos_base)
+    sc.oracle_q_norm_rope(pos_base)
+    sc.oracle_writeback(0, pos_base)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.attention(0, pos_base, is_prefill=True)
+    want = sc.oracle_attention(0, pos_base, is_prefill=True)
+    assert_attn_close(dev.out_f32(), want, f"prefill key split m={m} pos_base={pos_base} ksplit={ksplit}")

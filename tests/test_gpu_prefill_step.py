@@ -130,3 +130,16 @@ def test_prefill_step_then_decode_steps(cuda):
             for il in (0, 1):
                 dev.decode_step(il, pos)
         _same(dev_a, dev_b, f"decode step {step}")
+
+
+@pytest.mark.parametrize("m,pos", [(16, 3000), (70, 2500)])
+def test_prefill_step_key_split(cuda, m, pos):
+    """The fused step where the attention splits each tile's keys (short chunk,
+    long cache: chosen by grid size): same bits as the separate dispatches."""
+    _say(f"[prefill-step] key split m={m} pos={pos}")
+    sc = _scenario(m, pos, seed=5000 + m + pos)
+    dev_a = DeviceScenario(sc, upload_kv=True)
+    dev_b = DeviceScenario(sc, upload_kv=True)
+    _step(dev_a, 1, pos)
+    _unfused(dev_b, 1, pos)
+    _same(dev_a, dev_b, f"key split m={m} pos={pos}")

@@ -109,3 +109,22 @@ def test_prefill_step(cuda, kv, m, pos):
     assert np.array_equal(act[q], sc.act[q]), "normalized q differs"
     want = sc.oracle_attention(1, pos, is_prefill=True)
     assert_attn_close(dev.out_f32(), want, f"prefill step n_kv_head={kv} m={m} pos={pos}")
+
+
+@pytest.mark.parametrize("kv", KV_HEADS)
+def test_prefill_key_split(cuda, monkeypatch, kv):
+    """The key-split 4-wave layout (grid y = splits x 4 head sets) at this head count."""
+    monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", "1")
+    monkeypatch.setenv("BP_PREFILL_WG_WAVES", "4")
+    monkeypatch.setenv("BP_PREFILL_KSPLIT", "3")
+    _say(f"[heads] prefill key split n_kv_head={kv}")
+    cfg = _cfg(kv)
+    m, pos = 40, 1500
+    sc = Scenario(cfg, max_seq=pos + m + 3, m_tokens=m, seed=80 + kv)
+    _prefill_cache(sc, 0, pos, seed=90 + kv)
+    sc.oracle_q_norm_rope(pos)
+    sc.oracle_writeback(0, pos)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.attention(0, pos, is_prefill=True)
+    want = sc.oracle_attention(0, pos, is_prefill=True)
+    assert_attn_close(dev.out_f32(), want, f"prefill key split n_kv_head={kv}")

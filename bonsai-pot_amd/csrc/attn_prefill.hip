@@ -272,7 +272,8 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
 
 // Preparation pass of the fused prefill step (m_tokens new tokens at cache
 // rows [pos, pos + m_tokens)), in place of the dequantization pass. Grid (KV
-// head g, 64-row chunk c, part z), 512 threads:
+// head g, part y), 512 threads: y < n_chunks is part z = 0 of chunk c = y,
+// then parts z = 1 .. 4 of each chunk that holds new rows:
 //  z = 0: kv_writeback (kv_writeback_fused.wgsl) of the chunk's new rows of
 //     KV head g into the cache, their Q8_0 bytes and scales also kept in LDS
 //     (the chunk's other rows are read from the cache, rows < pos, or are
@@ -295,7 +296,14 @@ __global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillAr
     const int t = threadIdx.x;
     const int lane = t & 63, L = lane & (kItemLanes - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t g = blockIdx.x, c = blockIdx.y;
+    // y < n_chunks: part 0 of chunk y; then 4 parts q (1..4) for each chunk
+    // that holds new rows (from the one holding row pos on).
+    const uint32_t n_chunks = (a.n_rows + kChunk - 1) / kChunk;
+    const uint32_t g = blockIdx.x;
+    const uint32_t qi = blockIdx.y - n_chunks;   // wraps (large) for part 0
+    const bool q_part = blockIdx.y >= n_chunks;
+    const uint32_t c = q_part ? a.pos / kChunk + (qi >> 2) : blockIdx.y;
+    const uint32_t part = q_part ? 1 + (qi & 3) : 0u;
     const uint32_t row0 = c * kChunk;
     const uint32_t new_lo = max(row0, a.pos), new_hi = min(row0 + kChunk, a.pos + a.m_tokens);
     const bool k_half = wave < 4;                      // threads 0-255: K rows; 256-511: V
@@ -304,7 +312,7 @@ __global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillAr
     float kd, vd[4];
     uint2 vq[4];
     if (new_lo >= new_hi) {   // rows before pos only
-        if (blockIdx.z > 0) return;
+        if (part > 0) return;   // (not launched: q parts cover chunks with new rows only)
         if (k_half) {
             load_k_q8(a, g, c, th, kq0, kq1, kd);
             emit_k_rows(a, g, c, th, kq0, kq1, kd);
@@ -320,10 +328,10 @@ __global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillAr
     const uint32_t item_raw = 8 * wave + (lane >> 3);   // this lane's item (0..63)
     const bool live = item_raw < n_new;
     const uint32_t item = live ? item_raw : n_new - 1;  // dead items compute on a clamped one
-    if (blockIdx.z > 0) {
+    if (part > 0) {
         // ---- q_norm_rope of query head 4 g + z - 1, token tok0 + item ----
         const uint32_t tok = tok0 + item;
-        uint16_t* q = w.q_act + static_cast<uint64_t>(tok) * a.q_stride + (g * kGroup + blockIdx.z - 1) * kHeadDim;
+        uint16_t* q = w.q_act + static_cast<uint64_t>(tok) * a.q_stride + (g * kGroup + part - 1) * kHeadDim;
         const uint4 qx0 = *reinterpret_cast<const uint4*>(q + 8 * L);
         const uint4 qx1 = *reinterpret_cast<const uint4*>(q + 64 + 8 * L);
         const uint16_t* cs = w.rope_cs + static_cast<uint64_t>(a.pos + tok) * kHeadDim + 16 * L;
@@ -844,8 +852,10 @@ hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t 
 
 hipError_t launch_prefill_step(const PrefillArgs& a, const PrefillStepArgs& w, uint32_t n_kv_head, hipStream_t s,
                                bool prep_only) {
-    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk, 1 + kGroup),
-                       dim3(kPrepThreads), 0, s, a, w);
+    const uint32_t n_chunks = (a.n_rows + kChunk - 1) / kChunk;
+    const uint32_t new_chunks = n_chunks - a.pos / kChunk;   // chunks holding rows [pos, pos + m)
+    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, n_chunks + kGroup * new_chunks), dim3(kPrepThreads), 0, s,
+                       a, w);
     if (!prep_only) launch_attention(a, n_kv_head, s);
     return hipGetLastError();
 }

@@ -271,61 +271,66 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
 }
 
 // Preparation pass of the fused prefill step (m_tokens new tokens at cache
-// rows [pos, pos + m_tokens)), in place of the dequantization pass. Grid (KV
-// head g, part y), 512 threads: y < n_chunks is part z = 0 of chunk c = y,
-// then parts z = 1 .. 4 of each chunk that holds new rows:
-//  z = 0: kv_writeback (kv_writeback_fused.wgsl) of the chunk's new rows of
-//     KV head g into the cache, their Q8_0 bytes and scales also kept in LDS
-//     (the chunk's other rows are read from the cache, rows < pos, or are
-//     zero, rows past the last new row); then the chunk's image from those
-//     Q8_0 values, K rows by threads 0-255 while threads 256-511 transpose V.
-//     Chunks with no new row take their Q8_0 values from the cache directly.
+// rows [pos, pos + m_tokens)), in place of the dequantization pass. Work comes
+// in halves of 64-row chunks (32 rows). Grid (KV head g, part y), 256 threads:
+// y < n_halves (both halves of every chunk the image covers, so that it is
+// zero past n_rows) is part z = 0 of half y, then parts z = 1 .. 4 of each
+// half that holds new rows:
+//  z = 0: kv_writeback (kv_writeback_fused.wgsl) of the half's new rows of KV
+//     head g into the cache, their Q8_0 bytes and scales also kept in LDS
+//     (the half's other rows are read from the cache, rows < pos, or are zero,
+//     rows past the last new row); then the half's image from those Q8_0
+//     values, K rows by threads 0-127 while threads 128-255 transpose V.
+//     Halves with no new row take their Q8_0 values from the cache directly.
 //  z = 1 .. 4: q_norm_rope (q_norm_rope_fused.wgsl) of query head 4 g + z - 1
-//     for the chunk's new tokens, in place.
+//     for the half's new tokens, in place.
 // Both use the 8-lane item form of the standalone kernels (bp_norm_rope.hpp),
-// one item per 8 lanes (64 items: every new row or token of the chunk at
+// one item per 8 lanes (32 items: every new row or token of the half at
 // once), so q, the cache bytes and the image are bit for bit those of
 // q_norm_rope + kv_writeback + the dequantization pass. Every offset is
 // 8-element aligned (the host checks it), so all item loads and stores are 16
-// bytes.
-constexpr int kPrepThreads = 512;
-__global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillArgs a, PrefillStepArgs w) {
+// bytes. The image helpers take thread indices of a whole-chunk workgroup
+// (0..255): half h's K rows are those of threads 128 h .. +127, its V rows
+// those of emit_v_lds threads 128 h .. +127, and its V^T slots those of
+// emit_v_rows threads 2 d + h.
+constexpr int kPrepThreads = 256;
+constexpr int kHalf = kChunk / 2;
+__global__ __launch_bounds__(kPrepThreads, 4) void prefill_prep_kernel(PrefillArgs a, PrefillStepArgs w) {
     __shared__ __attribute__((aligned(16))) VTile vt;
-    __shared__ __attribute__((aligned(16))) uint8_t sq[2][kChunk][kHeadDim];   // K, V bytes of the chunk
-    __shared__ float sd[2][kChunk][kHeadDim / kBlock];                        // their scales
+    __shared__ __attribute__((aligned(16))) uint8_t sq[2][kHalf][kHeadDim];   // K, V bytes of the half
+    __shared__ float sd[2][kHalf][kHeadDim / kBlock];                        // their scales
     const int t = threadIdx.x;
     const int lane = t & 63, L = lane & (kItemLanes - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    // y < n_chunks: part 0 of chunk y; then 4 parts q (1..4) for each chunk
-    // that holds new rows (from the one holding row pos on).
-    const uint32_t n_chunks = (a.n_rows + kChunk - 1) / kChunk;
+    const uint32_t n_halves = 2 * ((a.n_rows + kChunk - 1) / kChunk);   // whole chunks: the image is zero past n_rows
     const uint32_t g = blockIdx.x;
-    const uint32_t qi = blockIdx.y - n_chunks;   // wraps (large) for part 0
-    const bool q_part = blockIdx.y >= n_chunks;
-    const uint32_t c = q_part ? a.pos / kChunk + (qi >> 2) : blockIdx.y;
+    const uint32_t qi = blockIdx.y - n_halves;   // wraps (large) for part 0
+    const bool q_part = blockIdx.y >= n_halves;
+    const uint32_t hc = q_part ? a.pos / kHalf + (qi >> 2) : blockIdx.y;   // half index
     const uint32_t part = q_part ? 1 + (qi & 3) : 0u;
-    const uint32_t row0 = c * kChunk;
-    const uint32_t new_lo = max(row0, a.pos), new_hi = min(row0 + kChunk, a.pos + a.m_tokens);
-    const bool k_half = wave < 4;                      // threads 0-255: K rows; 256-511: V
-    const int th = t & 255;
+    const uint32_t c = hc >> 1, half = hc & 1;   // chunk, and which half of it
+    const uint32_t row0 = hc * kHalf;
+    const uint32_t new_lo = max(row0, a.pos), new_hi = min(row0 + kHalf, a.pos + a.m_tokens);
+    const bool k_side = wave < 2;                 // threads 0-127: K rows; 128-255: V
+    const int tq = t & 127;                       // thread index within the side
+    const int tk = tq + 128 * half;               // emit_k_rows / emit_v_lds thread of this half
     U4 kq0, kq1;
     float kd, vd[4];
     uint2 vq[4];
-    if (new_lo >= new_hi) {   // rows before pos only
-        if (part > 0) return;   // (not launched: q parts cover chunks with new rows only)
-        if (k_half) {
-            load_k_q8(a, g, c, th, kq0, kq1, kd);
-            emit_k_rows(a, g, c, th, kq0, kq1, kd);
+    if (new_lo >= new_hi) {   // rows before pos only (q parts are launched for halves with new rows)
+        if (k_side) {
+            load_k_q8(a, g, c, tk, kq0, kq1, kd);
+            emit_k_rows(a, g, c, tk, kq0, kq1, kd);
         } else {
-            load_v_q8(a, g, c, th, vq, vd);
-            emit_v_lds(th, vq, vd, vt);
+            load_v_q8(a, g, c, tk, vq, vd);
+            emit_v_lds(tk, vq, vd, vt);
         }
         __syncthreads();
-        if (!k_half) emit_v_rows(a, g, c, th, vt);
+        if (!k_side) emit_v_rows(a, g, c, 2 * tq + half, vt);
         return;
     }
     const uint32_t n_new = new_hi - new_lo, tok0 = new_lo - a.pos;
-    const uint32_t item_raw = 8 * wave + (lane >> 3);   // this lane's item (0..63)
+    const uint32_t item_raw = 8 * wave + (lane >> 3);   // this lane's item (0..31)
     const bool live = item_raw < n_new;
     const uint32_t item = live ? item_raw : n_new - 1;  // dead items compute on a clamped one
     if (part > 0) {
@@ -349,15 +354,15 @@ __global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillAr
         return;
     }
     const uint32_t nb_row = a.kv_dim / kBlock;
-    // ---- loads first: the chunk's other rows (thread t -> K or V, row
-    // (t & 255) >> 2, block t & 3), then the new row of this lane's item ----
-    const uint32_t orr = th >> 2, okb = th & 3, orow = row0 + orr;
+    // ---- loads first: the half's other rows (thread -> K or V, row tq >> 2,
+    // block tq & 3), then the new row of this lane's item ----
+    const uint32_t orr = tq >> 2, okb = tq & 3, orow = row0 + orr;
     const bool other = orow < new_lo || orow >= new_hi;
     uint4 o0 = make_uint4(0, 0, 0, 0), o1 = o0;
     float od = 0.0f;
     if (other && orow < a.pos) {
-        const int8_t* qs = k_half ? a.k.qs : a.v.qs;
-        const float* dd = k_half ? a.k.d : a.v.d;
+        const int8_t* qs = k_side ? a.k.qs : a.v.qs;
+        const float* dd = k_side ? a.k.d : a.v.d;
         const uint64_t qo = static_cast<uint64_t>(orow) * a.kv_dim + g * kHeadDim + 32 * okb;
         o0 = *reinterpret_cast<const uint4*>(qs + qo);
         o1 = *reinterpret_cast<const uint4*>(qs + qo + 16);
@@ -409,33 +414,32 @@ __global__ __launch_bounds__(kPrepThreads, 2) void prefill_prep_kernel(PrefillAr
             }
         }
     }
-    // ---- the chunk's other rows into LDS (zero past the new rows) ----
+    // ---- the half's other rows into LDS (zero past the new rows) ----
     if (other) {
-        const int kv = k_half ? 0 : 1;
+        const int kv = k_side ? 0 : 1;
         *reinterpret_cast<uint4*>(&sq[kv][orr][32 * okb]) = o0;
         *reinterpret_cast<uint4*>(&sq[kv][orr][32 * okb + 16]) = o1;
         sd[kv][orr][okb] = od;
     }
     __syncthreads();
-    // ---- the image, from the chunk's Q8_0 values in LDS: K rows by threads
-    // 0-255, V^T by threads 256-511 ----
-    if (k_half) {
-        const int kr = th >> 2, kb = th & 3;
+    // ---- the image, from the half's Q8_0 values in LDS ----
+    if (k_side) {
+        const int kr = tq >> 2, kb = tq & 3;
         kq0 = *reinterpret_cast<const U4*>(&sq[0][kr][32 * kb]);
         kq1 = *reinterpret_cast<const U4*>(&sq[0][kr][32 * kb + 16]);
         kd = sd[0][kr][kb];
-        emit_k_rows(a, g, c, th, kq0, kq1, kd);
+        emit_k_rows(a, g, c, tk, kq0, kq1, kd);
     } else {
-        const int vq4 = th >> 4, vdg = th & 15;
+        const int vq4 = tq >> 4, vdg = tq & 15;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             vq[i] = *reinterpret_cast<const uint2*>(&sq[1][4 * vq4 + i][8 * vdg]);
             vd[i] = sd[1][4 * vq4 + i][vdg >> 2];
         }
-        emit_v_lds(th, vq, vd, vt);
+        emit_v_lds(tk, vq, vd, vt);
     }
     __syncthreads();
-    if (!k_half) emit_v_rows(a, g, c, th, vt);
+    if (!k_side) emit_v_rows(a, g, c, 2 * tq + half, vt);
 }
 
 // Layouts (kHpw query heads per wave, kWaves waves per workgroup):
@@ -852,9 +856,9 @@ hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t 
 
 hipError_t launch_prefill_step(const PrefillArgs& a, const PrefillStepArgs& w, uint32_t n_kv_head, hipStream_t s,
                                bool prep_only) {
-    const uint32_t n_chunks = (a.n_rows + kChunk - 1) / kChunk;
-    const uint32_t new_chunks = n_chunks - a.pos / kChunk;   // chunks holding rows [pos, pos + m)
-    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, n_chunks + kGroup * new_chunks), dim3(kPrepThreads), 0, s,
+    const uint32_t n_halves = 2 * ((a.n_rows + kChunk - 1) / kChunk);         // the image's chunks, whole
+    const uint32_t new_halves = (a.n_rows + kHalf - 1) / kHalf - a.pos / kHalf;   // halves holding rows [pos, pos + m)
+    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, n_halves + kGroup * new_halves), dim3(kPrepThreads), 0, s,
                        a, w);
     if (!prep_only) launch_attention(a, n_kv_head, s);
     return hipGetLastError();

@@ -809,24 +809,26 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
 }
 
 // Key-split merge: one wave per (token, query head); lane l combines dims
-// 2l, 2l + 1 of the n_ksplit partials by their log-sum-exp weights (as the
-// decode merge, attention_merge.wgsl:85-129) and stores f16(O / L).
+// 2l, 2l + 1 of the n_ksplit (<= 64) partials by their log-sum-exp weights (as
+// the decode merge, attention_merge.wgsl:85-129) and stores f16(O / L). Lane s
+// loads split s's (m, l) and computes its weight, so only the O loads loop.
 __global__ __launch_bounds__(64) void prefill_merge_kernel(PrefillArgs a) {
     const int lane = threadIdx.x;
     const uint32_t tok = blockIdx.x, h = blockIdx.y;
     const uint32_t n_head = a.q_stride / kHeadDim, ns = a.n_ksplit;
     const float* pp = a.kpart + (static_cast<uint64_t>(tok) * n_head + h) * ns * kSplitStride;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, pp[s * kSplitStride + kHeadDim]);
-    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    float2 ml = make_float2(-INFINITY, 0.0f);
+    if (static_cast<uint32_t>(lane) < ns) ml = *reinterpret_cast<const float2*>(pp + lane * kSplitStride + kHeadDim);
+    const float M = wave_max(ml.x);
+    const float w = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);   // 0 for splits without rows
+    const float L = wave_sum(w * ml.y);
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 8
     for (uint32_t s = 0; s < ns; s++) {
-        const float* q = pp + s * kSplitStride;
-        const float ms = q[kHeadDim];
-        const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);   // splits without rows
-        L = __builtin_fmaf(w, q[kHeadDim + 1], L);
-        const float2 v = *reinterpret_cast<const float2*>(q + 2 * lane);
-        o0 = __builtin_fmaf(w, v.x, o0);
-        o1 = __builtin_fmaf(w, v.y, o1);
+        const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+        const float2 v = *reinterpret_cast<const float2*>(pp + s * kSplitStride + 2 * lane);
+        o0 = __builtin_fmaf(ws, v.x, o0);
+        o1 = __builtin_fmaf(ws, v.y, o1);
     }
     const float inv_l = 1.0f / L;
     *reinterpret_cast<uint32_t*>(a.out + static_cast<uint64_t>(tok) * a.q_stride + h * kHeadDim + 2 * lane) =

@@ -548,6 +548,7 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
             uint32_t ns = m->prefill_ksplit != 0 ? m->prefill_ksplit
                                                   : std::min<uint32_t>(std::max<uint32_t>(cus / wgs, 1u), chunks / 8);
             const uint64_t cap = m->partials_floats / (static_cast<uint64_t>(m->cfg.n_head) * kPrefillSplitStride);
+            ns = std::min<uint32_t>(ns, 64);   // prefill_merge_kernel: one split per lane
             while (ns > 1 && static_cast<uint64_t>(m_tokens) * ns > cap) --ns;
             if (ns > 1) {
                 a.n_ksplit = ns;

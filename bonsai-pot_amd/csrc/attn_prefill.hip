@@ -98,8 +98,17 @@ __device__ __forceinline__ int fp6_scale_exp(float amax, int e_min) {
 // 32 floats / 2^e -> 32 fp6 e2m3 values (round to nearest even, saturating at
 // +-7.5) packed 6 bits each into 6 words. The hardware conversion takes two
 // 16-value halves and interleaves them: element 2j is v[j], 2j + 1 is v[16 + j].
+// Issued as inline asm with an early-clobber result: the compiler's builtin
+// may give the result registers that overlap the sources, and the instruction
+// then returns wrong values (measured on the box with dense inputs: every
+// element of a 32x32x64 product off; zero errors with disjoint registers).
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x6 __attribute__((ext_vector_type(6)));
+__device__ __forceinline__ i32x6 cvt_fp6x32(const f32x16& lo, const f32x16& hi, float scale) {
+    i32x6 r;
+    asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(r) : "v"(lo), "v"(hi), "v"(scale));
+    return r;
+}
 __device__ __forceinline__ i32x6 pack32_fp6(const float (&v)[32], int e) {
     f32x16 lo, hi;
 #pragma unroll
@@ -107,7 +116,7 @@ __device__ __forceinline__ i32x6 pack32_fp6(const float (&v)[32], int e) {
         lo[i] = v[i];
         hi[i] = v[16 + i];
     }
-    return __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23));
+    return cvt_fp6x32(lo, hi, __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23));
 }
 
 // Position of chunk row `key` (0..63) along the MFMA k axis of the PV step:
@@ -118,6 +127,12 @@ __device__ __forceinline__ int v_slot(int key) {
     const int s = k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3);
     return (key & 32) + s;
 }
+// The same for the 32x32x16 layout of prefill32_kernel: the S^T fragment of
+// lane (c, g) holds keys 8j + 4g + i (acc 4j + i) of a 32-key tile, and the
+// P^T operand of a 16-key step takes acc 8h .. 8h + 7 as its k slots
+// 8g .. 8g + 7, so slot 8g + e holds key 16h + 4g + (e & 3) + 8 (e >> 2):
+// within each 16 keys, bits 2 and 3 of the key index swapped.
+__device__ __forceinline__ int v_slot32(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
 // Bank-conflict swizzles of the staged chunk (no padding, so that the image
 // in global memory is the LDS image and a chunk is one linear copy):
 // 16-byte group j of K row r sits at group j ^ (r & 15); group j of V^T row
@@ -132,6 +147,14 @@ __device__ __forceinline__ int v_addr(int dim, int group) {
 __device__ __forceinline__ int l_addr(int row, int group) {
     return row * kHeadDim + 16 * (group ^ (row & 7));
 }
+// The image of prefill32_kernel stores each section group-major instead:
+// 16-byte group j of every row (dim) together, rows consecutive, so that the
+// 32 lanes of a fragment read 512 contiguous bytes (no bank conflicts, no
+// swizzle) and a lane's address for another group or row tile differs by a
+// constant (an instruction offset, not a register per fragment).
+__device__ __forceinline__ int k_addr32(int row, int group) { return (group * kChunk + row) * 8; }        // halves
+__device__ __forceinline__ int l_addr32(int row, int group) { return (group * kChunk + row) * 16; }       // bytes
+__device__ __forceinline__ int v_addr32(int dim, int group) { return (group * kHeadDim + dim) * 8; }     // halves
 
 // Maximum across the 4 lane groups of a token column (lanes l, l^16, l^32,
 // l^48), by lane-row swaps (no LDS round trip).
@@ -182,6 +205,37 @@ __device__ __forceinline__ void emit_k_rows(const PrefillArgs& a, uint32_t g, ui
         w[2 * i] = __builtin_bit_cast(uint32_t, f16x2{h[0], h[1]});
         w[2 * i + 1] = __builtin_bit_cast(uint32_t, f16x2{h[2], h[3]});
     }
+    if (a.vt_order) {
+        // prefill32_kernel's residual blocks follow its q.k fragments: block
+        // (m, h) = 2 m + h of a row holds dims 64 m + 16 j + 8 h + e (j, e <
+        // 4, 8), i.e. dims 8 h .. +7 and 16 + 8 h .. +7 of Q8_0 blocks 2 m and
+        // 2 m + 1 (this thread, kb, and its neighbour kb ^ 1, lanes t and
+        // t ^ 1). Thread kb builds block kb: it sends the neighbour the half
+        // of its values that the neighbour's block holds.
+        const bool odd = kb & 1;
+        float sent[16], got[16];
+#pragma unroll
+        for (int e2 = 0; e2 < 8; e2++) {
+            sent[e2] = r[(odd ? 0 : 8) + e2];
+            sent[8 + e2] = r[(odd ? 16 : 24) + e2];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) got[i] = lane_xor<1>(sent[i]);
+        float v[32];
+        amax = 0.0f;
+#pragma unroll
+        for (int e2 = 0; e2 < 8; e2++) {
+            v[e2] = odd ? got[e2] : r[e2];                  // j = 0: block 2m, dims 8h + e
+            v[8 + e2] = odd ? got[8 + e2] : r[16 + e2];     // j = 1: block 2m, dims 16 + 8h + e
+            v[16 + e2] = odd ? r[8 + e2] : got[e2];         // j = 2: block 2m+1, dims 8h + e
+            v[24 + e2] = odd ? r[24 + e2] : got[8 + e2];    // j = 3: block 2m+1, dims 16 + 8h + e
+        }
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            r[i] = v[i];
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+    }
     // block scale 2^e, applied by the MFMA as E8M0 e + 127 - 11 (>= 0)
     const int e = fp6_scale_exp(amax, kResidShift - kE8M0Bias);
     const i32x6 p6 = pack32_fp6(r, e);
@@ -191,15 +245,17 @@ __device__ __forceinline__ void emit_k_rows(const PrefillArgs& a, uint32_t g, ui
     uint16_t* kdst = a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        *reinterpret_cast<U4*>(kdst + k_addr(kr, 4 * kb + i)) = U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
+        *reinterpret_cast<U4*>(kdst + (a.vt_order ? k_addr32(kr, 4 * kb + i) : k_addr(kr, 4 * kb + i))) =
+            U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
     uint8_t* ldst = a.kl8 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kLBytes;
 #pragma unroll
     for (int i = 0; i < 2; i++)
-        *reinterpret_cast<U4*>(ldst + l_addr(kr, 2 * kb + i)) = U4{{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]}};
+        *reinterpret_cast<U4*>(ldst + (a.vt_order ? l_addr32(kr, 2 * kb + i) : l_addr(kr, 2 * kb + i))) =
+            U4{{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]}};
 }
-__device__ __forceinline__ void emit_v_lds(int t, const uint2 (&vq)[4], const float (&vd)[4], VTile& vt) {
+__device__ __forceinline__ void emit_v_lds(int t, const uint2 (&vq)[4], const float (&vd)[4], VTile& vt, bool o32) {
     const int vq4 = t >> 4, vdg = t & 15;
-    const int slot = v_slot(4 * vq4);   // rows 4 vq4 .. +3 -> slots slot .. slot + 3
+    const int slot = o32 ? v_slot32(4 * vq4) : v_slot(4 * vq4);   // rows 4 vq4 .. +3 -> slots slot .. slot + 3
 #pragma unroll
     for (int e = 0; e < 8; e++) {   // dim 8 vdg + e
         uint16_t hv[4];
@@ -218,7 +274,8 @@ __device__ __forceinline__ void emit_v_rows(const PrefillArgs& a, uint32_t g, ui
     uint16_t* vdst = a.vt16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kVHalves;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        *reinterpret_cast<U4*>(vdst + v_addr(dim, (s0 >> 3) + i)) = *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
+        *reinterpret_cast<U4*>(vdst + (a.vt_order ? v_addr32(dim, (s0 >> 3) + i) : v_addr(dim, (s0 >> 3) + i))) =
+            *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
 }
 
 // The Q8_0 inputs of emit_k_rows / emit_v_lds from the cache, for chunk c of
@@ -265,7 +322,7 @@ __global__ __launch_bounds__(256) void kv_dequant_kernel(PrefillArgs a) {
     load_k_q8(a, g, c, t, kq0, kq1, kd);
     load_v_q8(a, g, c, t, vq, vd);
     emit_k_rows(a, g, c, t, kq0, kq1, kd);
-    emit_v_lds(t, vq, vd, vt);
+    emit_v_lds(t, vq, vd, vt, a.vt_order != 0);
     __syncthreads();
     emit_v_rows(a, g, c, t, vt);
 }
@@ -323,7 +380,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void prefill_prep_kernel(PrefillAr
             emit_k_rows(a, g, c, tk, kq0, kq1, kd);
         } else {
             load_v_q8(a, g, c, tk, vq, vd);
-            emit_v_lds(tk, vq, vd, vt);
+            emit_v_lds(tk, vq, vd, vt, a.vt_order != 0);
         }
         __syncthreads();
         if (!k_side) emit_v_rows(a, g, c, 2 * tq + half, vt);
@@ -436,7 +493,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void prefill_prep_kernel(PrefillAr
             vq[i] = *reinterpret_cast<const uint2*>(&sq[1][4 * vq4 + i][8 * vdg]);
             vd[i] = sd[1][4 * vq4 + i][vdg >> 2];
         }
-        emit_v_lds(tk, vq, vd, vt);
+        emit_v_lds(tk, vq, vd, vt, a.vt_order != 0);
     }
     __syncthreads();
     if (!k_side) emit_v_rows(a, g, c, 2 * tq + half, vt);
@@ -835,11 +892,425 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(PrefillArgs a) {
         pack2(o0 * inv_l, o1 * inv_l);
 }
 
+// ============================================================================
+// prefill32_kernel: the same attention (same image, same arithmetic: f16 K
+// plus its fp6 residual, f16 V and P, f32 accumulation, exp2-domain online
+// softmax with the lazy max) on v_mfma_f32_32x32x16_f16, with the two waves
+// of each SIMD half an iteration apart so that one's softmax runs while the
+// other's MFMAs do.
+//
+//  * Workgroup: 8 waves, one KV head g and a zig-zag pair of 32-token tiles
+//    (light A = p, heavy B = n_tiles - 1 - p), processed one after the other,
+//    so every pair runs about (n_A + n_B) / 2 iterations. Wave w owns query
+//    head 4 g + (w & 3) for the tile's 32 tokens; "Y" waves (w >= 4) take the
+//    first half of the tile's key chunks, "X" waves (w < 4) the second half,
+//    and the halves are merged through LDS (log-sum-exp) at the end of the
+//    tile. Waves w and w + 4 share a SIMD.
+//  * Per 64-key chunk a wave runs an MFMA phase M(i) = S^T(i) = K Q^T (16
+//    32x32x16 MFMAs + 4 fp6 residual MFMAs) and O^T += V^T P^T(i-1) (16
+//    MFMAs), and a VALU phase V(i) = softmax of S^T(i) into P^T(i). Steps
+//    alternate: in step 2i the X waves run M(i) while the Y waves run
+//    V(i-1); in step 2i+1 the X waves run V(i) while the Y waves run M(i).
+//    A barrier (no memory fence) ends each step.
+//  * LDS: per stream (1: the Y waves' chunks, 2: the X waves') two K stages
+//    (K rows + residual, 24 KB) and two V^T stages (16 KB), each a separate
+//    object. A wave issues the copies of K(i+1) and V(i) of its own stream
+//    at the start of its VALU phase V(i) and waits for them at the barrier
+//    that ends it; they are first read in M(i+1).
+//  * Fragments (lane l, c = l % 32, g = l / 32): S^T / O^T acc 4j + i holds
+//    key (dim) 8j + 4g + i of token c; K / V^T operands hold row c, k slots
+//    8g .. 8g + 7 of the 16-wide step; the P^T operand of 16-key step
+//    h of a 32-key tile is acc 8h .. 8h + 7 (keys stored in V^T in v_slot32
+//    order). The residual MFMA m (k = 64) pairs lane (c, g)'s 32 values of
+//    residual block 2m + g of key c, dims 64m + 16j + 8g + e (the dims of its
+//    q.k fragments in k-steps 4m .. 4m + 3), with q of token c at the same
+//    dims, i.e. qb itself converted to fp6.
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32_resid(i32x8 a, i32x8 b, f32x16 c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 2, 2, 0, sa, 0, sb);
+}
+// Workgroup barriers without a memory fence (a workgroup-scope fence would
+// also wait for the copies still in flight). Before the first, this wave's
+// LDS reads are complete; before the second, also its copies into LDS.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void barrier_copies() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+constexpr int kKStage = kKHalves + kLBytes / 2;   // K rows then residual rows (24 KB)
+// x, as a value the compiler cannot see through (nor hoist what depends on it).
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+__global__ __launch_bounds__(512) void prefill32_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t k1a[kKStage], k1b[kKStage], k2a[kKStage], k2b[kKStage];
+    __shared__ __attribute__((aligned(16))) uint16_t v1a[kVHalves], v1b[kVHalves], v2a[kVHalves], v2b[kVHalves];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int c = lane & 31, g8 = lane >> 5;   // token column, k-slot group
+    const bool is_x = wave < 4;
+    const uint32_t g = blockIdx.x, pair = blockIdx.z;
+    const uint32_t head = g * kGroup + (wave & 3);
+    const float c2 = a.scale * 1.4426950408889634f;
+
+    // ---- per-tile state -------------------------------------------------------
+    uint32_t n_ch = 0, mid = 0;   // the tile's key chunks; Y: [0, mid), X: [mid, n_ch)
+    uint32_t wtok0 = 0, my_tok = 0, my_kend = 0, wave_kend = 0;
+    bool unit_live = false;
+    f16x8 qb[8];        // q of token my_tok, dims 16 ks + 8 g8 .. +7
+    i32x8 q6[2];        // qb[4 m .. 4 m + 3] as fp6 (residual block 2 m + g8), for the residual MFMAs
+    int q6s[2];         // their E8M0 scales
+    f32x16 o[4];        // O^T, dims 32 dt + 8 j + 4 g8 + i
+    f32x16 s[2];        // S^T of the current chunk, keys 32 kt + 8 j + 4 g8 + i
+    f16x8 pb[4];        // P^T of the last softmax, 16-key steps
+    float m_run = -INFINITY, l_run = 0.0f;   // l_run: this lane's keys only
+    bool have_p = false;
+
+    // Keys [0, kend) the tile attends, its 64-key chunks and the Y / X split.
+    auto tile_geom = [&](uint32_t tile, uint32_t& kend, uint32_t& n, uint32_t& md) __attribute__((always_inline)) {
+        const uint32_t last = min(tile * kPrefillTileTok + kPrefillTileTok, a.m_tokens) - 1;
+        kend = a.causal ? a.pos + last + 1 : a.pos;
+        n = (kend + kChunk - 1) / kChunk;
+        md = (n + 1) / 2;
+    };
+    // Loads of a tile's q into qb (waited for where they are used).
+    // Lanes of tokens past m_tokens load token 0's q: their scores are
+    // computed and never stored.
+    auto issue_q = [&](uint32_t tile) __attribute__((always_inline)) {
+        const uint32_t tok = tile * kPrefillTileTok + c;
+        const uint16_t* qp = a.q + static_cast<uint64_t>(tok < a.m_tokens ? tok : 0u) * a.q_stride + head * kHeadDim;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) qb[ks] = *reinterpret_cast<const f16x8*>(qp + 16 * ks + 8 * g8);
+    };
+    // Makes `tile` current: its token state, q as fp6 for the residual MFMAs,
+    // fresh accumulators.
+    auto enter_tile = [&](uint32_t tile) __attribute__((always_inline)) {
+        tile_geom(tile, wave_kend, n_ch, mid);
+        wtok0 = tile * kPrefillTileTok;
+        my_tok = wtok0 + c;
+        unit_live = wtok0 < a.m_tokens;
+        my_kend = a.causal ? a.pos + my_tok + 1 : a.pos;
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            float qf[32];
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {   // the lane's q.k dims of k-steps 4 m .. 4 m + 3
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    qf[8 * i + j] = static_cast<float>(qb[4 * m + i][j]);
+                    amax = fmaxf(amax, fabsf(qf[8 * i + j]));
+                }
+            }
+            const int e = fp6_scale_exp(amax, -126);
+            const i32x6 p6 = pack32_fp6(qf, e);
+            q6[m] = i32x8{p6[0], p6[1], p6[2], p6[3], p6[4], p6[5], 0, 0};
+            q6s[m] = e + kE8M0Bias;
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[dt] = f32x16{};
+        m_run = -INFINITY;
+        l_run = 0.0f;
+        have_p = false;
+    };
+    // f16(O / l) of this lane's token (l summed over the lane pair by the caller).
+    auto write_out = [&](float l_tot) __attribute__((always_inline)) {
+        if (!unit_live || my_tok >= a.m_tokens) return;
+        const float inv_l = 1.0f / l_tot;
+        uint16_t* out = a.out + static_cast<uint64_t>(my_tok) * a.q_stride + head * kHeadDim;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint2 w;
+                w.x = pack2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l);
+                w.y = pack2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l);
+                *reinterpret_cast<uint2*>(out + 32 * dt + 8 * j + 4 * g8) = w;
+            }
+    };
+
+    // ---- copies: 16-byte pieces, 1 KB per wave and instruction -------------
+    const uint16_t* k16 = a.k16 + static_cast<uint64_t>(g) * a.ws_chunks * kKHalves;
+    const uint16_t* vt16 = a.vt16 + static_cast<uint64_t>(g) * a.ws_chunks * kVHalves;
+    const uint8_t* kl8 = a.kl8 + static_cast<uint64_t>(g) * a.ws_chunks * kLBytes;
+    // Each copy moves the 1 KB at src (a uniform address) to LDS at dst,
+    // lane l's 16 bytes from src + 16 l. Issued as inline asm, so that the
+    // compiler neither tracks it nor waits for it before unrelated LDS reads:
+    // the waits are barrier_copies' (this wave's copies of the step).
+    const uint32_t lane16 = 16u * lane;
+    auto lds_copy = [&](const void* src, void* dst) __attribute__((always_inline)) {
+        const uint32_t lds = static_cast<uint32_t>(
+            reinterpret_cast<uintptr_t>((void __attribute__((address_space(3)))*)dst));
+        // (one wait state between the M0 write and the LDS DMA that reads it)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane16), "s"(src), "s"(lds)
+                     : "m0");
+    };
+    // The 4 waves of a role copy their role's chunks: wave (w & 3) moves the
+    // 1 KB pieces w & 3, +4, +8, ... of each section.
+    const int rw = wave & 3;
+    auto copy_k4 = [&](uint16_t* dst, uint32_t ch) __attribute__((always_inline)) {
+        const uint16_t* ks = k16 + static_cast<uint64_t>(ch) * kKHalves;
+        const uint8_t* ls = kl8 + static_cast<uint64_t>(ch) * kLBytes;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int piece = 64 * (4 * r + rw);
+            lds_copy(ks + 8 * piece, dst + 8 * piece);
+        }
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int piece = 64 * (4 * r + rw);
+            lds_copy(ls + 16 * piece, reinterpret_cast<uint8_t*>(dst + kKHalves) + 16 * piece);
+        }
+    };
+    auto copy_v4 = [&](uint16_t* dst, uint32_t ch) __attribute__((always_inline)) {
+        const uint16_t* vs = vt16 + static_cast<uint64_t>(ch) * kVHalves;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int piece = 64 * (4 * r + rw);
+            lds_copy(vs + 8 * piece, dst + 8 * piece);
+        }
+    };
+
+    // ---- MFMA phase pieces --------------------------------------------------
+    // Both MFMA blocks keep four LDS fragment reads in flight ahead of the
+    // MFMAs (sched_group_barrier: DS read = 0x100, MFMA = 0x008), so that
+    // the LDS latency hides behind the previous MFMAs. The lane parts of the
+    // fragment addresses (bytes) are made opaque at each use, so that the
+    // compiler forms each stage's addresses where it reads them instead of
+    // keeping a register per stage and fragment live across the loop.
+    const uint32_t lane_k = 2 * k_addr32(c, g8), lane_rv = l_addr32(c, 2 * g8);   // = 2 v_addr32(c, g8)
+    auto qk = [&](const uint16_t* kb) __attribute__((always_inline)) {
+        const uint8_t* kp = reinterpret_cast<const uint8_t*>(kb) + opaque(lane_k);
+        const uint8_t* lp = reinterpret_cast<const uint8_t*>(kb + kKHalves) + opaque(lane_rv);
+        f16x8 ka[16];   // fragment n: k-step n >> 1, key tile n & 1
+#pragma unroll
+        for (int n = 0; n < 16; n++)
+            ka[n] = *reinterpret_cast<const f16x8*>(kp + 2 * k_addr32(32 * (n & 1), 2 * (n >> 1)));
+        U4 r0[4], r1[4];   // residual of key tile n & 1, k block 2 (n >> 1) + g8
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const int row = 32 * (n & 1), blk = 2 * (n >> 1);
+            r0[n] = *reinterpret_cast<const U4*>(lp + l_addr32(row, 2 * blk));
+            r1[n] = *reinterpret_cast<const U4*>(lp + l_addr32(row, 2 * blk + 1));
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) s[kt] = f32x16{};
+#pragma unroll
+        for (int n = 0; n < 16; n++) s[n & 1] = mfma32(ka[n], qb[n >> 1], s[n & 1]);
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const i32x8 ra = {static_cast<int>(r0[n].w[0]), static_cast<int>(r0[n].w[1]), static_cast<int>(r0[n].w[2]),
+                              static_cast<int>(r0[n].w[3]), static_cast<int>(r1[n].w[0]), static_cast<int>(r1[n].w[1]), 0, 0};
+            s[n & 1] = mfma32_resid(ra, q6[n >> 1], s[n & 1], static_cast<int>(r1[n].w[2]), q6s[n >> 1]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int n = 0; n < 12; n++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+    auto pv = [&](const uint16_t* vb) __attribute__((always_inline)) {
+        const uint8_t* vp = reinterpret_cast<const uint8_t*>(vb) + opaque(lane_rv);
+        f16x8 va[16];   // fragment n: 16-key step n >> 2, dim tile n & 3
+#pragma unroll
+        for (int n = 0; n < 16; n++)
+            va[n] = *reinterpret_cast<const f16x8*>(vp + 2 * v_addr32(32 * (n & 3), 2 * (n >> 2)));
+#pragma unroll
+        for (int n = 0; n < 16; n++) o[n & 3] = mfma32(va[n], pb[n >> 2], o[n & 3]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int n = 0; n < 12; n++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+    // ---- VALU phase: mask, lazy running max, exponentials, P^T, row sums -----
+    auto softmax = [&](uint32_t key0) __attribute__((always_inline)) {
+        const bool need_mask = key0 + kChunk > (a.causal ? a.pos + wtok0 + 1 : a.pos);
+        if (need_mask) {
+            // key 32 kt + 8 j + 4 g8 + i of the chunk is visible while below
+            // my_kend - key0 (as integers); a masked score becomes -inf by a
+            // bit select on the sign of (my_kend - key0 - 1 - key): no compare
+            // masks (scalar registers) per element.
+            const int nv1 = static_cast<int>(my_kend - key0) - 1 - 4 * g8;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t dead = static_cast<uint32_t>((nv1 - (32 * kt + 8 * (r >> 2) + (r & 3))) >> 31);
+                    const float x = s[kt][r];   // (a bit cast of a vector element directly is miscompiled)
+                    s[kt][r] = __builtin_bit_cast(float, (dead & 0xFF800000u) | (~dead & __builtin_bit_cast(uint32_t, x)));
+                }
+        }
+        // (independent chains throughout: four partial maxima, the exponent
+        // arguments in place, then the exponentials, then packing, four
+        // partial row sums, so that no VALU result is waited for at once)
+        float pm[4];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const int kt = q4 >> 1, r0 = 8 * (q4 & 1);
+            pm[q4] = fmax_p(fmax_p(fmax_p(s[kt][r0], s[kt][r0 + 1]), fmax_p(s[kt][r0 + 2], s[kt][r0 + 3])),
+                            fmax_p(fmax_p(s[kt][r0 + 4], s[kt][r0 + 5]), fmax_p(s[kt][r0 + 6], s[kt][r0 + 7])));
+        }
+        const float lm = fmax_p(fmax_p(pm[0], pm[1]), fmax_p(pm[2], pm[3])) * c2;
+        if (__any(lm > m_run + kLazy)) {
+            const float cm = max_xor32(lm);   // the token's max over both lane groups
+            const bool up = cm > m_run + kLazy;
+            const float m_new = up ? cm : m_run;
+            const float alpha = up ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+        }
+        // m_run is still -inf only if every score of the token so far is
+        // masked (the X waves' chunks can all lie past an early token's last
+        // row): then p = exp2(-inf) = 0, not NaN.
+        const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[kt][r] = __builtin_fmaf(s[kt][r], c2, neg_m);
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[kt][r] = __builtin_amdgcn_exp2f(s[kt][r]);
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int kt = st >> 1, r0 = 8 * (st & 1);
+            U4 pk;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pk.w[i] = pack2_rne(s[kt][r0 + 2 * i], s[kt][r0 + 2 * i + 1]);
+                ls[i] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk.w[i]), f16x2{1, 1}, ls[i], false);
+            }
+            pb[st] = __builtin_bit_cast(f16x8, pk);
+        }
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    };
+
+    // ---- one tile ---------------------------------------------------------------
+    // The Y waves work on chunks [0, mid) from stream 1, the X waves on
+    // [mid, n_ch) from stream 2, and each role copies its own stream. Both run
+    // the same loop, iteration i = [copies of K(i+1) and V(i); M(i): P.V of
+    // i-1, then q.k of i; barrier; V(i): softmax of i; barrier], iterations
+    // 0 .. mid (the last only finishes the P.V of mid - 1); the Y waves run it
+    // one barrier later than the X waves, so that X's M phase meets Y's V
+    // phase and the other way round. Copies issued in an iteration's VALU
+    // phase are waited for at its end (K(i+1) and V(i) are first read in the
+    // next iteration's M phase).
+    // K(0) of this role's stream for `tile` (into stage 0) and its q loads:
+    // issued before the previous tile's merge, so that their latency hides
+    // behind it.
+    auto issue_tile = [&](uint32_t tile) __attribute__((always_inline)) {
+        uint32_t kend, n, md;
+        tile_geom(tile, kend, n, md);
+        const uint32_t ch0 = is_x ? md : 0u, cnt = is_x ? n - md : md;
+        if (cnt > 0) copy_k4(is_x ? k2a : k1a, ch0);
+        issue_q(tile);
+    };
+    auto process = [&]() __attribute__((always_inline)) {
+        const uint32_t ch0 = is_x ? mid : 0u;                // this role's first chunk
+        const uint32_t cnt = is_x ? n_ch - mid : mid;        // and its chunk count
+        uint16_t* const kst0 = is_x ? k2a : k1a;             // this role's stages
+        uint16_t* const kst1 = is_x ? k2b : k1b;
+        uint16_t* const vst0 = is_x ? v2a : v1a;
+        uint16_t* const vst1 = is_x ? v2b : v1b;
+        barrier_copies();              // K(0) (issue_tile) has landed
+        if (!is_x) barrier_copies();   // Y: one step behind
+        auto iter = [&](auto parc, uint32_t i) __attribute__((always_inline)) {
+            constexpr int par = decltype(parc)::value;
+            const bool live = unit_live && i < cnt && (ch0 + i) * kChunk < wave_kend;
+            if (have_p) {
+                pv(par ? vst0 : vst1);   // V(i-1)
+                have_p = false;
+            }
+            if (live) qk(par ? kst1 : kst0);
+            barrier_lds();
+            // copies at the start of the VALU phase (their issue would delay the
+            // MFMAs; here the other wave's MFMA phase covers it)
+            if (i + 1 < cnt) copy_k4(par ? kst0 : kst1, ch0 + i + 1);
+            if (i < cnt) copy_v4(par ? vst1 : vst0, ch0 + i);
+            if (live) {
+                softmax((ch0 + i) * kChunk);
+                have_p = true;
+            }
+            barrier_copies();
+        };
+        uint32_t i = 0;
+        for (; i + 1 <= mid; i += 2) {
+            iter(std::integral_constant<int, 0>{}, i);
+            iter(std::integral_constant<int, 1>{}, i + 1);
+        }
+        if (i <= mid) iter(std::integral_constant<int, 0>{}, i);
+        if (is_x) barrier_copies();   // X: the step Y is behind
+    };
+    // Merge: X hands (O, m, l) to Y through LDS (the V stages and K stage 1:
+    // K stage 0 may already receive the next tile's K(0)); Y stores f16(O / l).
+    auto merge = [&]() __attribute__((always_inline)) {
+        const float l_tot = sum_xor32(l_run);
+        float* xo = reinterpret_cast<float*>((wave & 3) == 0 ? v1a : (wave & 3) == 1 ? v1b : (wave & 3) == 2 ? v2a : v2b);
+        float* xml = reinterpret_cast<float*>(k1b) + (wave & 3) * 128;
+        if (is_x) {
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) xo[(dt * 16 + r) * 64 + lane] = o[dt][r];
+            if (lane < 32) {
+                xml[lane] = m_run;
+                xml[64 + lane] = l_tot;
+            }
+        }
+        barrier_lds();
+        if (!is_x) {
+            const float mx = xml[c], lx = xml[64 + c];
+            const float mm = fmaxf(m_run, mx);
+            const float ey = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - mm);
+            const float ex = mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mx - mm);
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[dt][r] = o[dt][r] * ey + xo[(dt * 16 + r) * 64 + lane] * ex;
+            write_out(l_tot * ey + lx * ex);
+        }
+        barrier_lds();   // the merge area is the next tile's stages
+    };
+
+    const uint32_t tile_a = pair, tile_b = a.n_tiles - 1 - pair;   // tile_b >= tile_a
+    issue_tile(tile_a);
+    enter_tile(tile_a);
+    for (uint32_t tile = tile_a;; tile = tile_b) {   // (one code instance for both tiles)
+        process();
+        const bool more = tile != tile_b;
+        if (more) issue_tile(tile_b);
+        merge();
+        if (!more) break;
+        enter_tile(tile_b);
+    }
+}
+
 }  // namespace
 
 static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
-    if (a.heads_per_wave == 2)
+    if (a.heads_per_wave == 2 && a.vt_order != 0)
+        hipLaunchKernelGGL(prefill32_kernel, dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
+    else if (a.heads_per_wave == 2)
         hipLaunchKernelGGL((prefill_kernel<2, 8>), dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
     else if (a.wg_waves == 4 && a.n_ksplit > 1) {
         hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4 * a.n_ksplit, a.n_tiles), dim3(256), 0, s, a);

@@ -112,6 +112,7 @@ struct PrefillArgs {
     uint16_t* vt16;
     uint8_t* kl8;
     uint32_t ws_chunks;       // 64-row chunks per KV head in the image
+    uint32_t vt_order;        // key order of V^T: 0 for prefill_kernel, 1 for prefill32_kernel
     uint32_t n_rows;          // rows the queries attend: cur of the last token
 };
 // Fused prefill step (q_norm_rope + kv_writeback + attention for the

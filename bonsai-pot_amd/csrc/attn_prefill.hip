@@ -1139,7 +1139,11 @@ __global__ __launch_bounds__(512) void prefill32_kernel(PrefillArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     };
     // ---- VALU phase: mask, lazy running max, exponentials, P^T, row sums -----
-    auto softmax = [&](uint32_t key0) __attribute__((always_inline)) {
+    // `hook(k)`, k = 0 .. 4, is called at five points spread over the VALU
+    // work (each issues two of the phase's copies: their issue then waits for
+    // the shared address unit between VALU instructions, not all at once).
+    auto softmax = [&](uint32_t key0, auto&& hook) __attribute__((always_inline)) {
+        hook(0);
         const bool need_mask = key0 + kChunk > (a.causal ? a.pos + wtok0 + 1 : a.pos);
         if (need_mask) {
             // key 32 kt + 8 j + 4 g8 + i of the chunk is visible while below
@@ -1167,6 +1171,7 @@ __global__ __launch_bounds__(512) void prefill32_kernel(PrefillArgs a) {
                             fmax_p(fmax_p(s[kt][r0 + 4], s[kt][r0 + 5]), fmax_p(s[kt][r0 + 6], s[kt][r0 + 7])));
         }
         const float lm = fmax_p(fmax_p(pm[0], pm[1]), fmax_p(pm[2], pm[3])) * c2;
+        hook(1);
         if (__any(lm > m_run + kLazy)) {
             const float cm = max_xor32(lm);   // the token's max over both lane groups
             const bool up = cm > m_run + kLazy;
@@ -1185,10 +1190,13 @@ __global__ __launch_bounds__(512) void prefill32_kernel(PrefillArgs a) {
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
             for (int r = 0; r < 16; r++) s[kt][r] = __builtin_fmaf(s[kt][r], c2, neg_m);
+        hook(2);
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+        for (int r = 0; r < 16; r++) s[0][r] = __builtin_amdgcn_exp2f(s[0][r]);
+        hook(3);
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[kt][r] = __builtin_amdgcn_exp2f(s[kt][r]);
+        for (int r = 0; r < 16; r++) s[1][r] = __builtin_amdgcn_exp2f(s[1][r]);
+        hook(4);
         float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < 4; st++) {
@@ -1242,13 +1250,32 @@ __global__ __launch_bounds__(512) void prefill32_kernel(PrefillArgs a) {
             }
             if (live) qk(par ? kst1 : kst0);
             barrier_lds();
-            // copies at the start of the VALU phase (their issue would delay the
-            // MFMAs; here the other wave's MFMA phase covers it)
-            if (i + 1 < cnt) copy_k4(par ? kst0 : kst1, ch0 + i + 1);
-            if (i < cnt) copy_v4(par ? vst1 : vst0, ch0 + i);
+            // K(i+1) and V(i) are copied during the VALU phase (their issue
+            // would delay the MFMAs; here the other wave's MFMA phase covers
+            // it): 10 copies of 1 KB, two at each softmax hook.
+            const bool k_on = i + 1 < cnt, v_on = i < cnt;
+            uint16_t* const kd = par ? kst0 : kst1;
+            uint16_t* const vd = par ? vst1 : vst0;
+            const uint16_t* const ks = k16 + static_cast<uint64_t>(ch0 + i + 1) * kKHalves;
+            const uint8_t* const ls = kl8 + static_cast<uint64_t>(ch0 + i + 1) * kLBytes;
+            const uint16_t* const vs = vt16 + static_cast<uint64_t>(ch0 + i) * kVHalves;
+            auto hook = [&](int k) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int n = 2 * k + j;   // 0-3: K rows, 4-5: K residual, 6-9: V^T
+                    const int piece = 64 * (4 * (n < 4 ? n : n < 6 ? n - 4 : n - 6) + rw);
+                    if (n < 4 && k_on) lds_copy(ks + 8 * piece, kd + 8 * piece);
+                    else if (n < 6 && k_on) lds_copy(ls + 16 * piece, reinterpret_cast<uint8_t*>(kd + kKHalves) + 16 * piece);
+                    else if (n >= 6 && v_on) lds_copy(vs + 8 * piece, vd + 8 * piece);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            };
             if (live) {
-                softmax((ch0 + i) * kChunk);
+                softmax((ch0 + i) * kChunk, hook);
                 have_p = true;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 5; k++) hook(k);
             }
             barrier_copies();
         };

@@ -26,6 +26,10 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "bonsai-pot_amd"))
+# The bench build of the library: the product library's kernels plus the
+# measurement hooks (include/bonsai_pot_hip_bench.h) this script times beside
+# them.
+os.environ.setdefault("BONSAI_POT_HIP_LIB", os.path.join(ROOT, "bonsai-pot_amd", "lib", "libbonsai_pot_hip_bench.so"))
 
 METRIC = "decode-attn HBM GB/s (%peak) ctx4K/32K; prefill-attn TFLOP/s (%MFMA) pp2048"
 HBM_PEAK_GBS = 8000.0
@@ -508,8 +512,12 @@ def measured_traffic(workload, kernel):
 
 
 def _cpu_info():
-    """CPU model name and the machine's physical core count (from /proc/cpuinfo)."""
-    name, cores = "unknown", set()
+    """CPU model of the host and its physical core count. The model name from
+    /proc/cpuinfo (a virtual machine may report only the vendor's family
+    name there), completed with the CPU family / model / stepping numbers and
+    lscpu's BIOS model name where they are available."""
+    import subprocess
+    name, cores, ids = "unknown", set(), {}
     try:
         phys = core = None
         with open("/proc/cpuinfo") as f:
@@ -518,6 +526,8 @@ def _cpu_info():
                 k, v = k.strip(), v.strip()
                 if k == "model name" and name == "unknown":
                     name = v
+                elif k in ("cpu family", "model", "stepping") and k not in ids:
+                    ids[k] = v
                 elif k == "physical id":
                     phys = v
                 elif k == "core id":
@@ -529,6 +539,19 @@ def _cpu_info():
             cores.add((phys, core))
     except OSError:
         pass
+    extra = []
+    if ids:
+        extra.append(", ".join(f"{k} {v}" for k, v in ids.items()))
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() == "BIOS Model name" and v.strip() and v.strip() != name:
+                extra.append("BIOS model name " + v.strip())
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if extra:
+        name = f"{name} ({'; '.join(extra)})"
     return name, len(cores) or None
 
 

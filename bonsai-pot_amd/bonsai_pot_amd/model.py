@@ -73,7 +73,6 @@ _SIGS = {
                                                   _u32]),
     "bp_dispatch_attention": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_attention_prefill_step": (_i32, [_vp, _vp, _vp] + [_u32] * 9),
-    "bp_debug_prefill_prep": (_i32, [_vp, _vp, _vp] + [_u32] * 9),
     "bp_dispatch_matvec_q1_0": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_matvec_q1_0_silu": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
     "bp_dispatch_matvec_q1_0_fused_normed": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
@@ -87,14 +86,20 @@ _SIGS = {
     "bp_kv_snapshot_apply": (_i32, [_vp, _u32, _vp, _u64]),
     "bp_attention_decode_noalloc": (_i32, [ctypes.POINTER(_Config), _vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32,
                                             _vp]),
-    "bp_debug_read_floor": (_i32, [_vp, _u64, _vp, _u32, _vp]),
     "bp_check_device": (_i32, [_vp]),
     "bp_debug_lose_device": (_i32, [_vp]),
     "bp_last_error": (ctypes.c_char_p, []),
     "bp_status_name": (ctypes.c_char_p, [_i32]),
 }
+# Measurement hooks of include/bonsai_pot_hip_bench.h, exported only by the
+# bench build (lib/libbonsai_pot_hip_bench.so, which bench.py loads).
+_BENCH_SIGS = {
+    "bp_debug_prefill_prep": (_i32, [_vp, _vp, _vp] + [_u32] * 9),
+    "bp_debug_read_floor": (_i32, [_vp, _u64, _vp, _u32, _vp]),
+}
 EXPORTED_SYMBOLS = tuple(_SIGS)
-for _name, (_res, _args) in _SIGS.items():
+BENCH_SYMBOLS = tuple(_BENCH_SIGS)
+for _name, (_res, _args) in list(_SIGS.items()) + [kv for kv in _BENCH_SIGS.items() if hasattr(lib, kv[0])]:
     _fn = getattr(lib, _name)
     _fn.restype = _res
     _fn.argtypes = _args
@@ -203,7 +208,8 @@ class Model:
     def debug_prefill_prep(self, act: int, w_norms: int, q_off: int, k_cur_off: int, v_cur_off: int,
                            out_off: int, w_q_norm_off: int, w_k_norm_off: int, layer_il: int, pos: int,
                            m_tokens: int) -> None:
-        """Measurement aid: the first launch of dispatch_attention_prefill_step alone."""
+        """Measurement aid (bench build of the library only): the first launch of
+        dispatch_attention_prefill_step alone."""
         _check(lib.bp_debug_prefill_prep(self._h, act, w_norms, q_off, k_cur_off, v_cur_off, out_off,
                                          w_q_norm_off, w_k_norm_off, layer_il, pos, m_tokens))
 

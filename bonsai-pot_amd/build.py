@@ -15,7 +15,13 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "lib", "libbonsai_pot_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
-SOURCES = ["bp_api.cpp", "norm_rope_writeback.hip", "attn_decode.hip", "attn_prefill.hip", "matvec_q1_0.hip", "matvec_q1_0_mfma.hip", "matmul_q1_0_q8_0.hip", "topk_reduce.hip", "read_floor.hip"]
+SOURCES = ["bp_api.cpp", "norm_rope_writeback.hip", "attn_decode.hip", "attn_prefill.hip", "matvec_q1_0.hip", "matvec_q1_0_mfma.hip", "matmul_q1_0_q8_0.hip", "topk_reduce.hip"]
+# The bench build (lib/libbonsai_pot_hip_bench.so, what bench.py loads): the
+# same kernel objects, bp_api.cpp compiled with BP_BENCH_HOOKS (the
+# measurement entry points of include/bonsai_pot_hip_bench.h) and the
+# read-floor kernel. The product library carries neither.
+BENCH_LIB = os.path.join(HERE, "lib", "libbonsai_pot_hip_bench.so")
+BENCH_SOURCES = {"bp_api_bench.o": ("bp_api.cpp", ["-DBP_BENCH_HOOKS"]), "read_floor.o": ("read_floor.hip", [])}
 # Per-source additions: the matmul's MFMA results go straight to VGPRs (the
 # default AGPR form costs one v_accvgpr_read per result element in its f32
 # epilogue); the decode kernels' leading scalar arguments (up to 14 dwords)
@@ -40,18 +46,26 @@ def _run(cmd):
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every kernel and the host layer, link the shared library, return its path."""
+    """Compile every kernel and the host layer, link the product library and
+    the bench build, return the product library's path."""
     obj_dir = os.path.join(HERE, "lib", "obj")
     os.makedirs(obj_dir, exist_ok=True)
     jobs = []
     for src in SOURCES:
         obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
         jobs.append((obj, [HIPCC, *FLAGS, *EXTRA_FLAGS.get(src, []), "-c", "-o", obj, os.path.join(CSRC, src)]))
-    with ThreadPoolExecutor(max_workers=min(4, len(jobs))) as ex:
-        list(ex.map(lambda j: _run(j[1]), jobs))
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB, *[o for o, _ in jobs]])
+    bench_jobs = []
+    for obj_name, (src, defs) in BENCH_SOURCES.items():
+        obj = os.path.join(obj_dir, obj_name)
+        bench_jobs.append((obj, [HIPCC, *FLAGS, *defs, "-c", "-o", obj, os.path.join(CSRC, src)]))
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        list(ex.map(lambda j: _run(j[1]), jobs + bench_jobs))
+    objs = [o for o, _ in jobs]
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB, *objs])
+    bench_objs = [o for o in objs if not o.endswith(os.sep + "bp_api.o")] + [o for o, _ in bench_jobs]
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", BENCH_LIB, *bench_objs])
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", BENCH_LIB)
     return LIB
 
 

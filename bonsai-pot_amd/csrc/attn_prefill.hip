@@ -1348,6 +1348,22 @@ static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream
         hipLaunchKernelGGL((prefill_kernel<1, 8>), dim3(n_kv_head, 2, n_pairs), dim3(512), 0, s, a);
 }
 
+// HIP's grid limit in y and z.
+constexpr uint64_t kGridYZMax = 65535;
+static uint64_t attention_grid_z(const PrefillArgs& a) {
+    return a.heads_per_wave == 1 && a.wg_waves == 4 && a.n_ksplit > 1 ? a.n_tiles : (a.n_tiles + 1) / 2;
+}
+static uint64_t prep_grid_y(const PrefillArgs& a) {
+    const uint64_t n_halves = 2 * ((static_cast<uint64_t>(a.n_rows) + kChunk - 1) / kChunk);
+    const uint64_t new_halves = (static_cast<uint64_t>(a.n_rows) + kHalf - 1) / kHalf - a.pos / kHalf;
+    return n_halves + kGroup * new_halves;
+}
+
+bool prefill_grid_fits(const PrefillArgs& a, bool step) {
+    const uint64_t y = step ? prep_grid_y(a) : (static_cast<uint64_t>(a.n_rows) + kChunk - 1) / kChunk;
+    return y <= kGridYZMax && attention_grid_z(a) <= kGridYZMax;
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
     hipLaunchKernelGGL(kv_dequant_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk), dim3(256), 0, s, a);
     launch_attention(a, n_kv_head, s);
@@ -1356,10 +1372,10 @@ hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t 
 
 hipError_t launch_prefill_step(const PrefillArgs& a, const PrefillStepArgs& w, uint32_t n_kv_head, hipStream_t s,
                                bool prep_only) {
-    const uint32_t n_halves = 2 * ((a.n_rows + kChunk - 1) / kChunk);         // the image's chunks, whole
-    const uint32_t new_halves = (a.n_rows + kHalf - 1) / kHalf - a.pos / kHalf;   // halves holding rows [pos, pos + m)
-    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, n_halves + kGroup * new_halves), dim3(kPrepThreads), 0, s,
-                       a, w);
+    // grid y: the image's chunks (two halves each), then kGroup q parts per
+    // half holding rows [pos, pos + m)
+    hipLaunchKernelGGL(prefill_prep_kernel, dim3(n_kv_head, static_cast<uint32_t>(prep_grid_y(a))), dim3(kPrepThreads),
+                       0, s, a, w);
     if (!prep_only) launch_attention(a, n_kv_head, s);
     return hipGetLastError();
 }

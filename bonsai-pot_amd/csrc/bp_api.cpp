@@ -12,6 +12,9 @@
 //   - the device-loss latch (src/model.rs:1087-1098, :1733-1751).
 // Kernels never allocate: everything a launch touches is created here once.
 #include "../../include/bonsai_pot_hip.h"
+#ifdef BP_BENCH_HOOKS
+#include "../../include/bonsai_pot_hip_bench.h"
+#endif
 
 #include <hip/hip_runtime.h>
 
@@ -348,9 +351,11 @@ bp_status bp_model_set_stream(bp_model* m, void* stream) {
     if (st != BP_OK) return st;
     // The model's scratch (split-K partials, normalized q, the prefill f16
     // image) is shared by every launch: work still queued on the old stream
-    // must finish before the new stream may reuse it.
+    // must finish before the new stream may reuse it. The whole device is
+    // drained, so that the old stream's handle is never used again (its owner
+    // may already have destroyed it).
     if (m->stream != static_cast<hipStream_t>(stream) &&
-        (st = hip_check(m, hipStreamSynchronize(m->stream), "set_stream: drain old stream")) != BP_OK)
+        (st = hip_check(m, hipDeviceSynchronize(), "set_stream: drain the device")) != BP_OK)
         return st;
     m->stream = static_cast<hipStream_t>(stream);
     return BP_OK;
@@ -580,6 +585,8 @@ bp_status bp_dispatch_attention(bp_model* m, void* act, uint32_t q_off, uint32_t
     if ((st = prefill_args(m, act, q_off, out_off, layer_il, pos, m_tokens, is_prefill, a)) != BP_OK ||
         a.m_tokens == 0)
         return st;
+    if (!bp::prefill_grid_fits(a, false))
+        return fail(BP_ERR_CONFIG, "attention: %u rows / %u tokens exceed the kernels' grid limits", a.n_rows, m_tokens);
     return hip_check(m, bp::launch_prefill(a, m->cfg.n_kv_head, m->stream), "attention launch");
 }
 
@@ -606,6 +613,9 @@ static bp_status prefill_step(bp_model* m, void* act, const void* w_norms, uint3
             return st;
         return bp_dispatch_attention(m, act, q_off, out_off, layer_il, pos, m_tokens, 1);
     }
+    if (!bp::prefill_grid_fits(a, true))
+        return fail(BP_ERR_CONFIG, "attention_prefill_step: %u rows / %u tokens exceed the kernels' grid limits",
+                    a.n_rows, m_tokens);
     bp::PrefillStepArgs w;
     w.q_act = static_cast<uint16_t*>(act) + q_off;
     w.k_cur = static_cast<const uint16_t*>(act) + k_cur_off;
@@ -631,12 +641,14 @@ bp_status bp_dispatch_attention_prefill_step(bp_model* m, void* act, const void*
                         pos, m_tokens, false);
 }
 
+#ifdef BP_BENCH_HOOKS
 bp_status bp_debug_prefill_prep(bp_model* m, void* act, const void* w_norms, uint32_t q_off, uint32_t k_cur_off,
                                 uint32_t v_cur_off, uint32_t out_off, uint32_t w_q_norm_off, uint32_t w_k_norm_off,
                                 uint32_t layer_il, uint32_t pos, uint32_t m_tokens) {
     return prefill_step(m, act, w_norms, q_off, k_cur_off, v_cur_off, out_off, w_q_norm_off, w_k_norm_off, layer_il,
                         pos, m_tokens, true);
 }
+#endif
 
 static bp_status matvec_common(bp_model* m, const void* weights, void* act, uint32_t k,
                                bp::MatvecArgs& a) {

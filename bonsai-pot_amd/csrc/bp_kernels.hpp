@@ -209,6 +209,9 @@ hipError_t launch_decode(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s)
 // Fused decode step: split pass (with q norm + row writeback) + merge pass.
 hipError_t launch_decode_step(const DecodeArgs& a, uint32_t n_kv_head, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s);
+// Whether the launches of launch_prefill (step = false) or launch_prefill_step
+// (step = true) for these arguments fit HIP's grid limits (y, z <= 65535).
+bool prefill_grid_fits(const PrefillArgs& a, bool step);
 // The fused prefill step: preparation pass (in place of the dequantization
 // pass) and attention, 2 launches; with prep_only the first launch alone.
 hipError_t launch_prefill_step(const PrefillArgs& a, const PrefillStepArgs& w, uint32_t n_kv_head, hipStream_t s,

@@ -2,11 +2,12 @@
 // device buffer once (grid-stride, all loads independent) and folds them into
 // one word per workgroup, so the compiler keeps every load. bench.py times it
 // over buffers of a decode's byte count to give the read floor the decode
-// kernels are compared with. Not part of the attention path.
+// kernels are compared with. Not part of the attention path: linked only
+// into the bench build of the library.
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
-#include "../../include/bonsai_pot_hip.h"
+#include "../../include/bonsai_pot_hip_bench.h"
 
 namespace {
 

@@ -81,8 +81,11 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
 void bp_model_destroy(bp_model* model);
 
 /* Stream all later calls are ordered on (a hipStream_t; NULL = the null stream).
- * Switching to another stream first waits for the old stream to drain, since
- * the model's scratch buffers are shared by all launches. */
+ * Switching to another stream first waits for the device to drain (all work
+ * queued so far, on any stream), since the model's scratch buffers are shared
+ * by all launches; the old stream's handle is not used, so it may already be
+ * destroyed. Not to be called while a stream of this device is being captured
+ * into a graph. */
 bp_status bp_model_set_stream(bp_model* model, void* stream);
 /* Blocks until the model's stream is idle; latches device loss on failure. */
 bp_status bp_model_synchronize(bp_model* model);
@@ -143,7 +146,9 @@ bp_status bp_dispatch_attention_decode_step(bp_model* model, void* act, const vo
  * [0, cur) with cur = is_prefill ? pos + m + 1 : pos. With pos == 0 and
  * is_prefill != 0 this is the reference's causal prefill from an empty cache;
  * pos > 0 is causal chunked prefill over an existing cache (the reference
- * reaches that result only one token at a time, src/forward.rs:914-967). */
+ * reaches that result only one token at a time, src/forward.rs:914-967).
+ * BP_ERR_CONFIG when the cache rows or tokens exceed the kernels' grid limits
+ * (more than 65535 64-row chunks, or 65535 pairs of 32-token tiles). */
 bp_status bp_dispatch_attention(bp_model* model, void* act, uint32_t q_off, uint32_t out_off,
                                 uint32_t layer_il, uint32_t pos, uint32_t m_tokens,
                                 uint32_t is_prefill);
@@ -159,7 +164,10 @@ bp_status bp_dispatch_attention(bp_model* model, void* act, uint32_t q_off, uint
  * queries and receives the normalized ones; cache rows [pos, pos+m_tokens)
  * receive the new K/V; act[out_off] receives the attention output. q_off and
  * out_off must be multiples of 8; when the other offsets are not (or act /
- * w_norms are not 16-byte aligned) the call runs the three dispatches above. */
+ * w_norms are not 16-byte aligned) the call runs the three dispatches above.
+ * BP_ERR_CONFIG when the preparation pass's grid would exceed 65535 in y
+ * (2 per 64-row chunk of the cache rows plus 4 per 32-row half holding the new
+ * rows: about 2 million rows), or as bp_dispatch_attention. */
 bp_status bp_dispatch_attention_prefill_step(bp_model* model, void* act, const void* w_norms,
                                              uint32_t q_off, uint32_t k_cur_off, uint32_t v_cur_off,
                                              uint32_t out_off, uint32_t w_q_norm_off,
@@ -260,24 +268,6 @@ bp_status bp_debug_lose_device(bp_model* model);
 bp_status bp_attention_decode_noalloc(const bp_config* cfg, void* kv_k, void* kv_v, uint32_t max_seq, void* act,
                                       uint32_t q_off, uint32_t out_off, uint32_t layer_il, uint32_t pos,
                                       void* stream);
-
-/* Measurement aid, no counterpart in the reference and not part of the
- * attention path: reads `bytes` (a multiple of 16) of device memory at `src`
- * once with independent 16-byte loads over `n_workgroups` workgroups of 256
- * threads and writes one word per workgroup to `sink` (n_workgroups x 4 bytes),
- * on `stream`. bench.py times it as the streaming-read floor of a decode's
- * byte count. */
-bp_status bp_debug_read_floor(const void* src, uint64_t bytes, void* sink, uint32_t n_workgroups, void* stream);
-
-/* Measurement aid, no counterpart in the reference: the first of the two
- * launches of bp_dispatch_attention_prefill_step alone (q norm + RoPE, the
- * K/V writeback and the attention kernel's f16 image of the layer's rows),
- * same arguments; every act / w_norms offset must be a multiple of 8.
- * bench.py times it to split the step's time between its two kernels. */
-bp_status bp_debug_prefill_prep(bp_model* model, void* act, const void* w_norms, uint32_t q_off,
-                                uint32_t k_cur_off, uint32_t v_cur_off, uint32_t out_off,
-                                uint32_t w_q_norm_off, uint32_t w_k_norm_off, uint32_t layer_il,
-                                uint32_t pos, uint32_t m_tokens);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* bp_last_error(void);

@@ -18,8 +18,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "bonsai_pot_hip.h")
 
 
-def declared_functions():
-    text = open(HEADER).read()
+BENCH_HEADER = os.path.join(ROOT, "include", "bonsai_pot_hip_bench.h")
+
+
+def declared_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(bp_[a-z0-9_]+)\s*\(", text)))
 
@@ -30,6 +33,20 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(bp.lib, n), f"{n} declared in include/ but not exported"
     assert set(names) == set(bp.EXPORTED_SYMBOLS)
+
+
+def test_bench_hooks_only_in_bench_build():
+    """The measurement hooks (include/bonsai_pot_hip_bench.h) are exported by
+    the bench build of the library and not by the product library."""
+    names = declared_functions(BENCH_HEADER)
+    assert set(names) == set(bp.model.BENCH_SYMBOLS)
+    product = ctypes.CDLL(os.path.join(os.path.dirname(bp.library_path), "libbonsai_pot_hip.so"))
+    bench = ctypes.CDLL(os.path.join(os.path.dirname(bp.library_path), "libbonsai_pot_hip_bench.so"))
+    for n in names:
+        assert not hasattr(product, n), f"{n} exported by the product library"
+        assert hasattr(bench, n), f"{n} missing from the bench build"
+    for n in declared_functions():
+        assert hasattr(bench, n), f"{n} missing from the bench build"
 
 
 def test_library_is_gfx950_hip_build():

@@ -184,8 +184,9 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 // residual of a block: 6 words of fp6, its E8M0 scale exponent less 11 in
 // word 6, word 7 zero), V keeps f16(v).
 typedef uint16_t VTile[kHeadDim][kChunk + 8];
-__device__ __forceinline__ void emit_k_rows(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const U4& kq0,
-                                            const U4& kq1, float kd) {
+// (The *_at forms write a chunk image at the given base: global memory or LDS.)
+__device__ __forceinline__ void emit_k_rows_at(uint16_t* kdst, uint8_t* ldst, uint32_t vt_order, int t, const U4& kq0,
+                                               const U4& kq1, float kd) {
     const int kr = t >> 2, kb = t & 3;
     uint32_t w[16];
     float r[32];
@@ -205,7 +206,7 @@ __device__ __forceinline__ void emit_k_rows(const PrefillArgs& a, uint32_t g, ui
         w[2 * i] = __builtin_bit_cast(uint32_t, f16x2{h[0], h[1]});
         w[2 * i + 1] = __builtin_bit_cast(uint32_t, f16x2{h[2], h[3]});
     }
-    if (a.vt_order) {
+    if (vt_order) {
         // prefill32_kernel's residual blocks follow its q.k fragments: block
         // (m, h) = 2 m + h of a row holds dims 64 m + 16 j + 8 h + e (j, e <
         // 4, 8), i.e. dims 8 h .. +7 and 16 + 8 h .. +7 of Q8_0 blocks 2 m and
@@ -242,16 +243,19 @@ __device__ __forceinline__ void emit_k_rows(const PrefillArgs& a, uint32_t g, ui
     const uint32_t lo[8] = {static_cast<uint32_t>(p6[0]), static_cast<uint32_t>(p6[1]), static_cast<uint32_t>(p6[2]),
                             static_cast<uint32_t>(p6[3]), static_cast<uint32_t>(p6[4]), static_cast<uint32_t>(p6[5]),
                             static_cast<uint32_t>(e + kE8M0Bias - kResidShift), 0u};
-    uint16_t* kdst = a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        *reinterpret_cast<U4*>(kdst + (a.vt_order ? k_addr32(kr, 4 * kb + i) : k_addr(kr, 4 * kb + i))) =
+        *reinterpret_cast<U4*>(kdst + (vt_order ? k_addr32(kr, 4 * kb + i) : k_addr(kr, 4 * kb + i))) =
             U4{{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]}};
-    uint8_t* ldst = a.kl8 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kLBytes;
 #pragma unroll
     for (int i = 0; i < 2; i++)
-        *reinterpret_cast<U4*>(ldst + (a.vt_order ? l_addr32(kr, 2 * kb + i) : l_addr(kr, 2 * kb + i))) =
+        *reinterpret_cast<U4*>(ldst + (vt_order ? l_addr32(kr, 2 * kb + i) : l_addr(kr, 2 * kb + i))) =
             U4{{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]}};
+}
+__device__ __forceinline__ void emit_k_rows(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const U4& kq0,
+                                            const U4& kq1, float kd) {
+    emit_k_rows_at(a.k16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kKHalves,
+                   a.kl8 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kLBytes, a.vt_order, t, kq0, kq1, kd);
 }
 __device__ __forceinline__ void emit_v_lds(int t, const uint2 (&vq)[4], const float (&vd)[4], VTile& vt, bool o32) {
     const int vq4 = t >> 4, vdg = t & 15;
@@ -269,13 +273,15 @@ __device__ __forceinline__ void emit_v_lds(int t, const uint2 (&vq)[4], const fl
             make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16), hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
     }
 }
-__device__ __forceinline__ void emit_v_rows(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const VTile& vt) {
+__device__ __forceinline__ void emit_v_rows_at(uint16_t* vdst, uint32_t vt_order, int t, const VTile& vt) {
     const int dim = t >> 1, s0 = 32 * (t & 1);
-    uint16_t* vdst = a.vt16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kVHalves;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        *reinterpret_cast<U4*>(vdst + (a.vt_order ? v_addr32(dim, (s0 >> 3) + i) : v_addr(dim, (s0 >> 3) + i))) =
+        *reinterpret_cast<U4*>(vdst + (vt_order ? v_addr32(dim, (s0 >> 3) + i) : v_addr(dim, (s0 >> 3) + i))) =
             *reinterpret_cast<const U4*>(&vt[dim][s0 + 8 * i]);
+}
+__device__ __forceinline__ void emit_v_rows(const PrefillArgs& a, uint32_t g, uint32_t c, int t, const VTile& vt) {
+    emit_v_rows_at(a.vt16 + (static_cast<uint64_t>(g) * a.ws_chunks + c) * kVHalves, a.vt_order, t, vt);
 }
 
 // The Q8_0 inputs of emit_k_rows / emit_v_lds from the cache, for chunk c of
@@ -359,11 +365,14 @@ __global__ __launch_bounds__(kPrepThreads, 4) void prefill_prep_kernel(PrefillAr
     const int t = threadIdx.x;
     const int lane = t & 63, L = lane & (kItemLanes - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t n_halves = 2 * ((a.n_rows + kChunk - 1) / kChunk);   // whole chunks: the image is zero past n_rows
+    // part-0 halves: every half of the image (whole chunks: the image is zero
+    // past n_rows), or with no image (direct) those holding new rows
+    const uint32_t half0 = a.direct ? a.pos / kHalf : 0u;
+    const uint32_t n_halves = a.direct ? (a.n_rows + kHalf - 1) / kHalf - half0 : 2 * ((a.n_rows + kChunk - 1) / kChunk);
     const uint32_t g = blockIdx.x;
     const uint32_t qi = blockIdx.y - n_halves;   // wraps (large) for part 0
     const bool q_part = blockIdx.y >= n_halves;
-    const uint32_t hc = q_part ? a.pos / kHalf + (qi >> 2) : blockIdx.y;   // half index
+    const uint32_t hc = q_part ? a.pos / kHalf + (qi >> 2) : half0 + blockIdx.y;   // half index
     const uint32_t part = q_part ? 1 + (qi & 3) : 0u;
     const uint32_t c = hc >> 1, half = hc & 1;   // chunk, and which half of it
     const uint32_t row0 = hc * kHalf;
@@ -417,7 +426,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void prefill_prep_kernel(PrefillAr
     const bool other = orow < new_lo || orow >= new_hi;
     uint4 o0 = make_uint4(0, 0, 0, 0), o1 = o0;
     float od = 0.0f;
-    if (other && orow < a.pos) {
+    if (other && orow < a.pos && !a.direct) {
         const int8_t* qs = k_side ? a.k.qs : a.v.qs;
         const float* dd = k_side ? a.k.d : a.v.d;
         const uint64_t qo = static_cast<uint64_t>(orow) * a.kv_dim + g * kHeadDim + 32 * okb;
@@ -471,6 +480,7 @@ __global__ __launch_bounds__(kPrepThreads, 4) void prefill_prep_kernel(PrefillAr
             }
         }
     }
+    if (a.direct) return;   // no image
     // ---- the half's other rows into LDS (zero past the new rows) ----
     if (other) {
         const int kv = k_side ? 0 : 1;
@@ -865,31 +875,45 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
     write_unit();
 }
 
-// Key-split merge: one wave per (token, query head); lane l combines dims
-// 2l, 2l + 1 of the n_ksplit (<= 64) partials by their log-sum-exp weights (as
-// the decode merge, attention_merge.wgsl:85-129) and stores f16(O / L). Lane s
-// loads split s's (m, l) and computes its weight, so only the O loads loop.
+// Key-split merge: one wave per (token, query head) combines the n_ksplit
+// (<= 64) partials by their log-sum-exp weights (as the decode merge,
+// attention_merge.wgsl:85-129) and stores f16(O / L). Lane l reads dims
+// 4 (l & 31) .. +3 of splits 2 k + (l >> 5), k < kLoads, all loads issued at
+// once (past n_ksplit: the last split again, weight 0); lane s < n_ksplit
+// holds split s's (m, l), its weight is fetched by a lane permute.
+template <int kLoads>
 __global__ __launch_bounds__(64) void prefill_merge_kernel(PrefillArgs a) {
     const int lane = threadIdx.x;
     const uint32_t tok = blockIdx.x, h = blockIdx.y;
     const uint32_t n_head = a.q_stride / kHeadDim, ns = a.n_ksplit;
     const float* pp = a.kpart + (static_cast<uint64_t>(tok) * n_head + h) * ns * kSplitStride;
+    const int half = lane >> 5, d4 = 4 * (lane & 31);
+    f32x4 ov[kLoads];
+#pragma unroll
+    for (int k = 0; k < kLoads; k++) {
+        const uint32_t sp = min(static_cast<uint32_t>(2 * k + half), ns - 1);
+        ov[k] = *reinterpret_cast<const f32x4*>(pp + sp * kSplitStride + d4);
+    }
     float2 ml = make_float2(-INFINITY, 0.0f);
     if (static_cast<uint32_t>(lane) < ns) ml = *reinterpret_cast<const float2*>(pp + lane * kSplitStride + kHeadDim);
     const float M = wave_max(ml.x);
     const float w = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);   // 0 for splits without rows
     const float L = wave_sum(w * ml.y);
-    float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll 8
-    for (uint32_t s = 0; s < ns; s++) {
-        const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
-        const float2 v = *reinterpret_cast<const float2*>(pp + s * kSplitStride + 2 * lane);
-        o0 = __builtin_fmaf(ws, v.x, o0);
-        o1 = __builtin_fmaf(ws, v.y, o1);
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < kLoads; k++) {
+        const float wk = __shfl(w, 2 * k + half);   // lanes >= ns hold weight 0
+        acc += wk * ov[k];
     }
-    const float inv_l = 1.0f / L;
-    *reinterpret_cast<uint32_t*>(a.out + static_cast<uint64_t>(tok) * a.q_stride + h * kHeadDim + 2 * lane) =
-        pack2(o0 * inv_l, o1 * inv_l);
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] += __shfl_xor(acc[i], 32);
+    if (half == 0) {
+        const float inv_l = 1.0f / L;
+        uint2 o;
+        o.x = pack2(acc[0] * inv_l, acc[1] * inv_l);
+        o.y = pack2(acc[2] * inv_l, acc[3] * inv_l);
+        *reinterpret_cast<uint2*>(a.out + static_cast<uint64_t>(tok) * a.q_stride + h * kHeadDim + d4) = o;
+    }
 }
 
 // ============================================================================
@@ -1331,17 +1355,320 @@ __global__ __launch_bounds__(512) void prefill32_kernel(PrefillArgs a) {
     }
 }
 
+// ============================================================================
+// prefill_split_kernel: short chunks over long caches (few query tiles, many
+// cache rows), split over the keys. Same arithmetic as prefill32_kernel (f16
+// K plus its fp6 residual, f16 V and P, f32 accumulation, exp2-domain online
+// softmax with the lazy max, the same 32x32x16 fragments), but the workgroup
+// reads the layer's Q8_0 rows from the cache itself instead of a prepared
+// image, so a call touches each cache row once instead of re-imaging the
+// whole layer:
+//  * Grid (KV head g, key split s, tile pair z); 8 waves. Wave w owns query
+//    head 4 g + (w & 3) for the 32 tokens of tile 2 z + (w >> 2), so the
+//    workgroup's 8 waves share one stream of chunks: rows of split s, i.e.
+//    64-row chunks [s * split_chunks, +split_chunks) of those the pair's last
+//    token attends.
+//  * Per chunk: its Q8_0 bytes and scales (18 KB) are copied into LDS by
+//    global_load_lds (18 copies of 1 KB spread over the waves), issued two
+//    chunks ahead; waves 0-3 convert the K rows (emit_k_rows: f16 rows and
+//    the fp6 residual) and waves 4-7 transpose V (emit_v_lds, then
+//    emit_v_rows after a barrier) into the compute stage of the next chunk
+//    while every wave computes on the current one (S^T = K Q^T, softmax, O^T
+//    += V^T P^T), double-buffered.
+//  * Each wave writes its partial (O unnormalized, m in log2 units, l) per
+//    token to kpart; prefill_merge_kernel combines the splits.
+__global__ __launch_bounds__(512) void prefill_split_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t stk[2][kKStage];    // K rows + residual, per stage
+    __shared__ __attribute__((aligned(16))) uint16_t stv[2][kVHalves];   // V^T, per stage
+    __shared__ __attribute__((aligned(16))) uint8_t rq[2][2][kChunk][kHeadDim];          // [buf][K, V][row]: Q8_0 bytes
+    __shared__ __attribute__((aligned(16))) float rd[2][2][kChunk][kHeadDim / kBlock];   // and scales
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int c = lane & 31, g8 = lane >> 5;
+    const uint32_t g = blockIdx.x, split = blockIdx.y, tpair = blockIdx.z;
+    const uint32_t tile = 2 * tpair + (wave >> 2);
+    const uint32_t head = g * kGroup + (wave & 3);
+    const uint32_t wtok0 = tile * kPrefillTileTok;
+    const bool unit_live = wtok0 < a.m_tokens;
+    const uint32_t my_tok = wtok0 + c;
+    const uint32_t my_kend = a.pos + my_tok + 1;   // causal: token m attends rows [0, pos + m]
+    const uint32_t wave_kend = unit_live ? a.pos + min(wtok0 + kPrefillTileTok, a.m_tokens) : 0u;
+    const uint32_t pair_kend = a.pos + min(2 * kPrefillTileTok * (tpair + 1), a.m_tokens);
+    const uint32_t n_ch = (pair_kend + kChunk - 1) / kChunk;
+    const uint32_t c0 = min(split * a.split_chunks, n_ch), cnt = min(c0 + a.split_chunks, n_ch) - c0;
+
+    // ---- q of this lane's token (tokens past m_tokens load token 0's) ----------
+    f16x8 qb[8];
+    {
+        const uint16_t* qp = a.q + static_cast<uint64_t>(my_tok < a.m_tokens ? my_tok : 0u) * a.q_stride +
+                             head * kHeadDim;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) qb[ks] = *reinterpret_cast<const f16x8*>(qp + 16 * ks + 8 * g8);
+    }
+
+    // ---- copies of a chunk's Q8_0 rows into raw buffer b: copy n (0..17) by
+    // wave n % 8: n < 8 K bytes of rows 8 n .. +7, 8..15 V bytes, 16 / 17 the
+    // K / V scales of the 64 rows (rows past n_rows: the last row again) ----
+    const uint32_t nb_row = a.kv_dim / kBlock;
+    const uint32_t last_row = a.n_rows - 1;
+    auto dma = [&](uint32_t ch, int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const int n = wave + 8 * k;
+            if (n >= 18) break;
+            const bool is_v = (n >= 8 && n < 16) || n == 17;
+            const char* base;
+            uint32_t off;
+            uint32_t lds;
+            if (n < 16) {
+                const uint32_t row = min(ch * kChunk + 8 * (n & 7) + (lane >> 3), last_row);
+                off = row * a.kv_dim + 16 * (lane & 7);
+                base = reinterpret_cast<const char*>(is_v ? a.v.qs : a.k.qs) + g * kHeadDim;
+                lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                    (void __attribute__((address_space(3)))*)&rq[b][is_v][8 * (n & 7)][0]));
+            } else {
+                const uint32_t row = min(ch * kChunk + lane, last_row);
+                off = row * nb_row * 4;
+                base = reinterpret_cast<const char*>(is_v ? a.v.d : a.k.d) + g * (kHeadDim / kBlock) * 4;
+                lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                    (void __attribute__((address_space(3)))*)&rd[b][is_v][0][0]));
+            }
+            // (one wait state between the M0 write and the LDS DMA that reads it)
+            lds = __builtin_amdgcn_readfirstlane(lds);   // uniform (the compiler cannot tell)
+            asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                         : "m0");
+        }
+    };
+    // ---- the chunk in raw buffer b into compute stage st: K rows by waves
+    // 0-3 (emit_k_rows), V^T by waves 4-7: thread (dims 4 dq .. +3, 16-byte
+    // group j of V^T, i.e. slots 8 j .. +7 holding keys v_slot32(slot)) reads
+    // the 4 bytes of those dims of the 8 keys, writes 4 groups ----
+    auto emit = [&](int b, int st) __attribute__((always_inline)) {
+        if (t < 256) {
+            const int kr = t >> 2, kb = t & 3;
+            const U4 kq0 = *reinterpret_cast<const U4*>(&rq[b][0][kr][32 * kb]);
+            const U4 kq1 = *reinterpret_cast<const U4*>(&rq[b][0][kr][32 * kb + 16]);
+            emit_k_rows_at(stk[st], reinterpret_cast<uint8_t*>(stk[st] + kKHalves), 1u, t, kq0, kq1, rd[b][0][kr][kb]);
+        } else {
+            const int tv = t - 256, dq = tv & 31, j = tv >> 5;
+            uint32_t x[8];
+            float d[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int key = v_slot32(8 * j + e);   // (v_slot32 is its own inverse)
+                x[e] = *reinterpret_cast<const uint32_t*>(&rq[b][1][key][4 * dq]);
+                d[e] = rd[b][1][key][dq >> 3];
+            }
+            __builtin_amdgcn_sched_barrier(0);   // all 16 reads in flight before the first wait
+#pragma unroll
+            for (int n = 0; n < 4; n++) {
+                const int dd = (n + dq + (dq >> 2)) & 3;   // rotated: fewer bank conflicts between lanes
+                U4 grp;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const float v0 = d[e] * static_cast<float>(static_cast<int8_t>(x[e] >> (8 * dd)));
+                    const float v1 = d[e + 1] * static_cast<float>(static_cast<int8_t>(x[e + 1] >> (8 * dd)));
+                    grp.w[e >> 1] = pack2_rne(v0, v1);
+                }
+                *reinterpret_cast<U4*>(stv[st] + v_addr32(4 * dq + dd, j)) = grp;
+            }
+        }
+    };
+
+    // ---- q as fp6 for the residual MFMAs (as prefill32_kernel's enter_tile) ----
+    i32x8 q6[2];
+    int q6s[2];
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        float qf[32];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                qf[8 * i + j] = static_cast<float>(qb[4 * m + i][j]);
+                amax = fmaxf(amax, fabsf(qf[8 * i + j]));
+            }
+        const int e = fp6_scale_exp(amax, -126);
+        const i32x6 p6 = pack32_fp6(qf, e);
+        q6[m] = i32x8{p6[0], p6[1], p6[2], p6[3], p6[4], p6[5], 0, 0};
+        q6s[m] = e + kE8M0Bias;
+    }
+    f32x16 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) o[dt] = f32x16{};
+    f32x16 s[2];
+    f16x8 pb[4];
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float c2 = a.scale * 1.4426950408889634f;
+
+    // ---- compute on a stage (the fragments of prefill32_kernel) ----
+    const uint32_t lane_k = 2 * k_addr32(c, g8), lane_rv = l_addr32(c, 2 * g8);
+    auto qk = [&](const uint16_t* kb) __attribute__((always_inline)) {
+        const uint8_t* kp = reinterpret_cast<const uint8_t*>(kb) + opaque(lane_k);
+        const uint8_t* lp = reinterpret_cast<const uint8_t*>(kb + kKHalves) + opaque(lane_rv);
+        f16x8 ka[16];
+#pragma unroll
+        for (int n = 0; n < 16; n++)
+            ka[n] = *reinterpret_cast<const f16x8*>(kp + 2 * k_addr32(32 * (n & 1), 2 * (n >> 1)));
+        U4 r0[4], r1[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const int row = 32 * (n & 1), blk = 2 * (n >> 1);
+            r0[n] = *reinterpret_cast<const U4*>(lp + l_addr32(row, 2 * blk));
+            r1[n] = *reinterpret_cast<const U4*>(lp + l_addr32(row, 2 * blk + 1));
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) s[kt] = f32x16{};
+#pragma unroll
+        for (int n = 0; n < 16; n++) s[n & 1] = mfma32(ka[n], qb[n >> 1], s[n & 1]);
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const i32x8 ra = {static_cast<int>(r0[n].w[0]), static_cast<int>(r0[n].w[1]), static_cast<int>(r0[n].w[2]),
+                              static_cast<int>(r0[n].w[3]), static_cast<int>(r1[n].w[0]), static_cast<int>(r1[n].w[1]), 0, 0};
+            s[n & 1] = mfma32_resid(ra, q6[n >> 1], s[n & 1], static_cast<int>(r1[n].w[2]), q6s[n >> 1]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int n = 0; n < 12; n++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+    auto pv = [&](const uint16_t* vb) __attribute__((always_inline)) {
+        const uint8_t* vp = reinterpret_cast<const uint8_t*>(vb) + opaque(lane_rv);
+        f16x8 va[16];
+#pragma unroll
+        for (int n = 0; n < 16; n++)
+            va[n] = *reinterpret_cast<const f16x8*>(vp + 2 * v_addr32(32 * (n & 3), 2 * (n >> 2)));
+#pragma unroll
+        for (int n = 0; n < 16; n++) o[n & 3] = mfma32(va[n], pb[n >> 2], o[n & 3]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int n = 0; n < 12; n++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
+    auto softmax = [&](uint32_t key0) __attribute__((always_inline)) {
+        if (key0 + kChunk > a.pos + wtok0 + 1) {   // some key past the wave's first token's last row
+            const int nv1 = static_cast<int>(my_kend - key0) - 1 - 4 * g8;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t dead = static_cast<uint32_t>((nv1 - (32 * kt + 8 * (r >> 2) + (r & 3))) >> 31);
+                    const float x = s[kt][r];   // (a bit cast of a vector element directly is miscompiled)
+                    s[kt][r] = __builtin_bit_cast(float, (dead & 0xFF800000u) | (~dead & __builtin_bit_cast(uint32_t, x)));
+                }
+        }
+        float pm[4];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const int kt = q4 >> 1, r0 = 8 * (q4 & 1);
+            pm[q4] = fmax_p(fmax_p(fmax_p(s[kt][r0], s[kt][r0 + 1]), fmax_p(s[kt][r0 + 2], s[kt][r0 + 3])),
+                            fmax_p(fmax_p(s[kt][r0 + 4], s[kt][r0 + 5]), fmax_p(s[kt][r0 + 6], s[kt][r0 + 7])));
+        }
+        const float lm = fmax_p(fmax_p(pm[0], pm[1]), fmax_p(pm[2], pm[3])) * c2;
+        if (__any(lm > m_run + kLazy)) {
+            const float cm = max_xor32(lm);
+            const bool up = cm > m_run + kLazy;
+            const float m_new = up ? cm : m_run;
+            const float alpha = up ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+        }
+        const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], c2, neg_m));
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int kt = st >> 1, r0 = 8 * (st & 1);
+            U4 pk;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pk.w[i] = pack2_rne(s[kt][r0 + 2 * i], s[kt][r0 + 2 * i + 1]);
+                ls[i] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk.w[i]), f16x2{1, 1}, ls[i], false);
+            }
+            pb[st] = __builtin_bit_cast(f16x8, pk);
+        }
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    };
+
+    // ---- the chunk loop: iteration i computes chunk c0 + i from stage i & 1,
+    // converts chunk c0 + i + 1 into the other stage and copies chunk c0 + i + 2
+    // into the raw buffer chunk c0 + i held ----
+    if (cnt > 0) dma(c0, 0);
+    if (cnt > 1) dma(c0 + 1, 1);
+    barrier_copies();
+    if (cnt > 0) emit(0, 0);
+    for (uint32_t i = 0; i < cnt; i++) {
+        const int st = static_cast<int>(i & 1);
+        barrier_copies();   // stage st complete; raw chunk i + 1 landed
+        if (i + 2 < cnt) dma(c0 + i + 2, st);
+        if (i + 1 < cnt) emit(1 - st, 1 - st);
+        const uint32_t key0 = (c0 + i) * kChunk;
+        if (unit_live && key0 < wave_kend) {
+            qk(stk[st]);
+            softmax(key0);
+            pv(stv[st]);
+        }
+    }
+
+    // ---- partial of this split: O (unnormalized), m (log2 units), l ----
+    const float l_tot = sum_xor32(l_run);
+    if (!unit_live || my_tok >= a.m_tokens) return;
+    const uint32_t n_head = a.q_stride / kHeadDim;
+    float* pp = a.kpart + ((static_cast<uint64_t>(my_tok) * n_head + head) * a.n_ksplit + split) * kSplitStride;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *reinterpret_cast<f32x4*>(pp + 32 * dt + 8 * j + 4 * g8) =
+                f32x4{o[dt][4 * j], o[dt][4 * j + 1], o[dt][4 * j + 2], o[dt][4 * j + 3]};
+    if (g8 == 0) *reinterpret_cast<float2*>(pp + kHeadDim) = make_float2(m_run, l_tot);
+}
+
 }  // namespace
+
+static void launch_prefill_merge(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
+    const dim3 grid(a.m_tokens, n_kv_head * kGroup);
+    if (a.n_ksplit <= 8)
+        hipLaunchKernelGGL(prefill_merge_kernel<4>, grid, dim3(64), 0, s, a);
+    else if (a.n_ksplit <= 16)
+        hipLaunchKernelGGL(prefill_merge_kernel<8>, grid, dim3(64), 0, s, a);
+    else if (a.n_ksplit <= 32)
+        hipLaunchKernelGGL(prefill_merge_kernel<16>, grid, dim3(64), 0, s, a);
+    else
+        hipLaunchKernelGGL(prefill_merge_kernel<32>, grid, dim3(64), 0, s, a);
+}
 
 static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
     const uint32_t n_pairs = (a.n_tiles + 1) / 2;
-    if (a.heads_per_wave == 2 && a.vt_order != 0)
+    if (a.direct) {
+        hipLaunchKernelGGL(prefill_split_kernel, dim3(n_kv_head, a.n_ksplit, n_pairs), dim3(512), 0, s, a);
+        launch_prefill_merge(a, n_kv_head, s);
+    } else if (a.heads_per_wave == 2 && a.vt_order != 0)
         hipLaunchKernelGGL(prefill32_kernel, dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
     else if (a.heads_per_wave == 2)
         hipLaunchKernelGGL((prefill_kernel<2, 8>), dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
     else if (a.wg_waves == 4 && a.n_ksplit > 1) {
         hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4 * a.n_ksplit, a.n_tiles), dim3(256), 0, s, a);
-        hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.m_tokens, n_kv_head * kGroup), dim3(64), 0, s, a);
+        launch_prefill_merge(a, n_kv_head, s);
     } else if (a.wg_waves == 4)
         hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4, n_pairs), dim3(256), 0, s, a);
     else
@@ -1351,21 +1678,24 @@ static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream
 // HIP's grid limit in y and z.
 constexpr uint64_t kGridYZMax = 65535;
 static uint64_t attention_grid_z(const PrefillArgs& a) {
-    return a.heads_per_wave == 1 && a.wg_waves == 4 && a.n_ksplit > 1 ? a.n_tiles : (a.n_tiles + 1) / 2;
+    return a.heads_per_wave == 1 && a.wg_waves == 4 && a.n_ksplit > 1 && !a.direct ? a.n_tiles : (a.n_tiles + 1) / 2;
 }
+// Preparation pass, grid y: the image's halves (or with no image, the halves
+// holding new rows), then kGroup q parts per half holding new rows.
 static uint64_t prep_grid_y(const PrefillArgs& a) {
-    const uint64_t n_halves = 2 * ((static_cast<uint64_t>(a.n_rows) + kChunk - 1) / kChunk);
     const uint64_t new_halves = (static_cast<uint64_t>(a.n_rows) + kHalf - 1) / kHalf - a.pos / kHalf;
+    const uint64_t n_halves = a.direct ? new_halves : 2 * ((static_cast<uint64_t>(a.n_rows) + kChunk - 1) / kChunk);
     return n_halves + kGroup * new_halves;
 }
 
 bool prefill_grid_fits(const PrefillArgs& a, bool step) {
-    const uint64_t y = step ? prep_grid_y(a) : (static_cast<uint64_t>(a.n_rows) + kChunk - 1) / kChunk;
+    const uint64_t y = step ? prep_grid_y(a) : a.direct ? 0 : (static_cast<uint64_t>(a.n_rows) + kChunk - 1) / kChunk;
     return y <= kGridYZMax && attention_grid_z(a) <= kGridYZMax;
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, uint32_t n_kv_head, hipStream_t s) {
-    hipLaunchKernelGGL(kv_dequant_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk), dim3(256), 0, s, a);
+    if (!a.direct)
+        hipLaunchKernelGGL(kv_dequant_kernel, dim3(n_kv_head, (a.n_rows + kChunk - 1) / kChunk), dim3(256), 0, s, a);
     launch_attention(a, n_kv_head, s);
     return hipGetLastError();
 }

@@ -550,17 +550,23 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
         a.n_ksplit = 1;
         a.split_chunks = 0;
         a.kpart = m->partials;
+        a.direct = 0;
         if (a.heads_per_wave == 1 && a.wg_waves == 4 && is_prefill) {
+            // prefill_split_kernel: one 8-wave workgroup per (KV head, key
+            // split, tile pair) reading the cache rows itself; enough splits
+            // to give every CU a workgroup, at least 2 chunks each.
             const uint32_t chunks = static_cast<uint32_t>((rows + 63) / 64);   // the last tile's key chunks
-            const uint32_t wgs = a.n_tiles * 4 * m->cfg.n_kv_head;           // workgroups per split
-            uint32_t ns = m->prefill_ksplit != 0 ? m->prefill_ksplit
-                                                  : std::min<uint32_t>(std::max<uint32_t>(cus / wgs, 1u), chunks / 8);
+            const uint32_t wgs = pairs * m->cfg.n_kv_head;                   // workgroups per split
+            uint32_t ns = m->prefill_ksplit != 0
+                              ? m->prefill_ksplit
+                              : std::min<uint32_t>(std::max<uint32_t>((cus + wgs - 1) / wgs, 1u), chunks / 2);
             const uint64_t cap = m->partials_floats / (static_cast<uint64_t>(m->cfg.n_head) * kPrefillSplitStride);
             ns = std::min<uint32_t>(ns, 64);   // prefill_merge_kernel: one split per lane
             while (ns > 1 && static_cast<uint64_t>(m_tokens) * ns > cap) --ns;
             if (ns > 1) {
                 a.n_ksplit = ns;
                 a.split_chunks = (chunks + ns - 1) / ns;
+                a.direct = 1;
             }
         }
     }

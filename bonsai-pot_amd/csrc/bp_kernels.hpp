@@ -114,6 +114,10 @@ struct PrefillArgs {
     uint32_t ws_chunks;       // 64-row chunks per KV head in the image
     uint32_t vt_order;        // key order of V^T: 0 for prefill_kernel, 1 for prefill32_kernel
     uint32_t n_rows;          // rows the queries attend: cur of the last token
+    // 1: the key split runs prefill_split_kernel, which reads the cache's
+    // Q8_0 rows itself: no image is written (the dequantization pass is
+    // skipped and the preparation pass only writes the new rows and q).
+    uint32_t direct;
 };
 // Fused prefill step (q_norm_rope + kv_writeback + attention for the
 // m_tokens tokens at cache rows [pos, pos + m_tokens)): what the preparation
@@ -134,7 +138,7 @@ struct PrefillStepArgs {
 };
 // Token x split products the key-split partials are sized for (the host
 // picks n_ksplit within it).
-constexpr uint32_t kPrefillSplitTok = 512;
+constexpr uint32_t kPrefillSplitTok = 2048;
 // Bytes of the K/V image for max_seq rows (one layer): f16 K, f16 V^T and
 // the K residual, 640 bytes per (row, KV head).
 inline uint64_t prefill_image_bytes(uint32_t n_kv_head, uint32_t max_seq) {

@@ -319,10 +319,11 @@ def test_config1_real_cache_last_layer(cuda):
                                                (70, 2500, "auto"), (70, 2500, "7"), (100, 5, "4"),
                                                (33, 31, "2"), (64, 640, "40")])
 def test_prefill_key_split(cuda, monkeypatch, m, pos_base, ksplit):
-    """Short chunks over long caches: the 4-wave layout splits every tile's key
-    range over several workgroups and merges their partials (forced split
-    counts include ones whose last splits lie past some tiles' keys, and one
-    above the chunk count)."""
+    """Short chunks over long caches: prefill_split_kernel splits the keys over
+    several workgroups, each reading the cache rows itself, and
+    prefill_merge_kernel combines their partials (forced split counts include
+    ones whose last splits lie past some tiles' keys, and one above the chunk
+    count)."""
     monkeypatch.setenv("BP_PREFILL_HEADS_PER_WAVE", "1")
     monkeypatch.setenv("BP_PREFILL_WG_WAVES", "4")
     if ksplit != "auto":

@@ -533,14 +533,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
     // heads each XCD serves one head and its L2 holds that head's K/V for all
     // the head's tile pairs. (Grid dimensions instead of a 1-D id: no integer
     // divisions at the kernel's start.)
-    // With a key split (a.n_ksplit > 1, 4-wave layout only) the grid is (KV
-    // head, split x 4 + head set, tile): each workgroup takes one tile
-    // (self-paired) and the key chunks [c_lo, c_lo + split_chunks) of it.
-    constexpr uint32_t kSets = kWaves == 4 ? 4 : 2 / kHpw;   // head sets per KV head
-    const bool ksplit = kWaves == 4 && a.n_ksplit > 1;
     const uint32_t g = blockIdx.x, pair = blockIdx.z;
-    const uint32_t hs = ksplit ? blockIdx.y % kSets : blockIdx.y, ks = ksplit ? blockIdx.y / kSets : 0u;
-    const uint32_t tile_a = pair, tile_b = ksplit ? pair : a.n_tiles - 1 - pair;   // tile_b >= tile_a
+    const uint32_t hs = blockIdx.y;   // head set
+    const uint32_t tile_a = pair, tile_b = a.n_tiles - 1 - pair;   // tile_b >= tile_a
     const uint32_t h0 = kWaves == 4 ? g * kGroup + hs   // first query head
                                     : g * kGroup + 2 * hs + kHeadsPerWave * ((wave >> 1) & 1);
     const uint32_t utok = 16 * (wave & 1);            // unit's first token within its tile
@@ -553,8 +548,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
     };
     const uint32_t kend_b = tile_kend(tile_b);
     const uint32_t n_tot = (kend_b + kChunk - 1) / kChunk;   // chunks tile B attends
-    const uint32_t c_lo = ksplit ? min(ks * a.split_chunks, n_tot) : 0u;
-    const uint32_t n_b = ksplit ? min(a.split_chunks, n_tot - c_lo) : n_tot;   // this workgroup's share
+    constexpr uint32_t c_lo = 0;
+    const uint32_t n_b = n_tot;
     const uint32_t n_a = tile_b == tile_a ? 0u : (tile_kend(tile_a) + kChunk - 1) / kChunk;
     const uint32_t mid = (n_a + n_b + 1) / 2;        // B waves: [0, mid); A waves: [mid, n_b) of B
     const uint32_t n_iter = mid;                     // >= n_a + (n_b - mid)
@@ -857,20 +852,6 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
             m_fin[h] = mm;
         }
         l_run[h] = lb;
-    }
-    if (ksplit) {
-        // partial (O unnormalized, m in log2 units, l) of this key split
-        if (!unit_live || my_tok >= a.m_tokens) return;
-        const uint32_t n_head = a.q_stride / kHeadDim;
-#pragma unroll
-        for (int h = 0; h < kHeadsPerWave; h++) {
-            float* pp = a.kpart + ((static_cast<uint64_t>(my_tok) * n_head + h0 + h) * a.n_ksplit + ks) * kSplitStride;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++)
-                *reinterpret_cast<f32x4*>(pp + 16 * dt + 4 * lg) = o[h][dt];
-            if (lg == 0) *reinterpret_cast<float2*>(pp + kHeadDim) = make_float2(m_fin[h], l_run[h]);
-        }
-        return;
     }
     write_unit();
 }
@@ -1666,10 +1647,7 @@ static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream
         hipLaunchKernelGGL(prefill32_kernel, dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
     else if (a.heads_per_wave == 2)
         hipLaunchKernelGGL((prefill_kernel<2, 8>), dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
-    else if (a.wg_waves == 4 && a.n_ksplit > 1) {
-        hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4 * a.n_ksplit, a.n_tiles), dim3(256), 0, s, a);
-        launch_prefill_merge(a, n_kv_head, s);
-    } else if (a.wg_waves == 4)
+    else if (a.wg_waves == 4)
         hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4, n_pairs), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL((prefill_kernel<1, 8>), dim3(n_kv_head, 2, n_pairs), dim3(512), 0, s, a);
@@ -1678,7 +1656,7 @@ static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream
 // HIP's grid limit in y and z.
 constexpr uint64_t kGridYZMax = 65535;
 static uint64_t attention_grid_z(const PrefillArgs& a) {
-    return a.heads_per_wave == 1 && a.wg_waves == 4 && a.n_ksplit > 1 && !a.direct ? a.n_tiles : (a.n_tiles + 1) / 2;
+    return (a.n_tiles + 1) / 2;
 }
 // Preparation pass, grid y: the image's halves (or with no image, the halves
 // holding new rows), then kGroup q parts per half holding new rows.

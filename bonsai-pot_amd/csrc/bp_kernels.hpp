@@ -91,11 +91,11 @@ struct PrefillArgs {
     uint32_t n_tiles;         // ceil(m_tokens / kPrefillTileTok)
     uint32_t heads_per_wave;  // prefill_kernel layout: 2, or 1 (two or four workgroups per tile pair)
     uint32_t wg_waves;        // with 1 head per wave: 8 (two head sets) or 4 (four, one head each)
-    // Key split (short chunks over long caches): n_ksplit > 1 workgroups per
-    // (tile, KV head, head set), each over split_chunks 64-row chunks of the
-    // tile's key range, write partial (O, m, l) to kpart, [m][n_head][n_ksplit]
-    // x 132 floats (O, m, l, pad); prefill_merge_kernel combines them. 4-wave
-    // layout only.
+    // Key split (short chunks over long caches, with direct = 1): n_ksplit > 1
+    // workgroups of prefill_split_kernel per (KV head, tile pair), each over
+    // split_chunks 64-row chunks of the pair's key range, write partial (O, m,
+    // l) to kpart, [m][n_head][n_ksplit] x 132 floats (O, m, l, pad);
+    // prefill_merge_kernel combines them.
     uint32_t n_ksplit;
     uint32_t split_chunks;
     float* kpart;

@@ -551,11 +551,13 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
         a.split_chunks = 0;
         a.kpart = m->partials;
         a.direct = 0;
-        if (a.heads_per_wave == 1 && a.wg_waves == 4 && is_prefill) {
-            // prefill_split_kernel: one 8-wave workgroup per (KV head, key
+        const uint32_t chunks = static_cast<uint32_t>((rows + 63) / 64);   // the last tile's key chunks
+        if (a.heads_per_wave == 1 && a.wg_waves == 4 && is_prefill &&
+            (m->prefill_ksplit != 0 || chunks >= 4 * a.n_tiles)) {
+            // prefill_split_kernel for few tiles over a long cache (at least 4
+            // key chunks per tile): one 8-wave workgroup per (KV head, key
             // split, tile pair) reading the cache rows itself; enough splits
             // to give every CU a workgroup, at least 2 chunks each.
-            const uint32_t chunks = static_cast<uint32_t>((rows + 63) / 64);   // the last tile's key chunks
             const uint32_t wgs = pairs * m->cfg.n_kv_head;                   // workgroups per split
             uint32_t ns = m->prefill_ksplit != 0
                               ? m->prefill_ksplit

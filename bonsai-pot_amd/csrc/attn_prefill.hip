@@ -2,24 +2,29 @@
 //
 // Same result as src/shaders/attention.wgsl (reference repository) — token m
 // attends rows [0, cur) with cur = causal ? pos + m + 1 : pos, f32 softmax,
-// f16 output — computed in two passes:
+// f16 output. Three forms, chosen by the host from the shapes:
 //
-// kv_dequant_kernel writes the layer's K and V for rows [0, cur of the last
-// token) as an f16 image (f16(d * q) per value, plus a K residual below): per
-// KV head and 64-row chunk, K rows and V^T (dims x key slots in the MFMA order
-// below), 16-byte groups XOR-swizzled against LDS bank conflicts, so that a
-// chunk is one linear copy.
+// 1. Image pass + prefill32_kernel (long prompts): kv_dequant_kernel (or the
+//    fused step's prefill_prep_kernel) writes the layer's K and V for rows
+//    [0, cur of the last token) as an f16 image (f16(d * q) per value, plus a
+//    K residual below), per KV head and 64-row chunk laid out as its LDS
+//    image, so that a chunk is one linear copy; prefill32_kernel runs on
+//    v_mfma_f32_32x32x16_f16 with 4 query heads x 32 tokens per role and the
+//    two waves of each SIMD one phase apart (its own comment below).
+// 2. Image pass + prefill_kernel<1, 8> / <1, 4> (shorter prompts): one query
+//    head per wave on v_mfma_f32_16x16x32_f16, two or four workgroups per
+//    (KV head, tile pair), so that small grids still fill the CUs.
+// 3. prefill_split_kernel + prefill_merge_kernel (few tokens over a long
+//    cache): the keys split over workgroups that read the cache's Q8_0 rows
+//    themselves (no image), partials merged by their log-sum-exp weights.
 //
-// prefill_kernel, a flash-attention over LDS tiles of that image:
-//  * Query tokens form tiles of 32; a "unit" is 16 tokens x 2 GQA heads (one
-//    wave's MFMA columns). A 512-thread workgroup owns one KV head and a
-//    zig-zag PAIR of tiles: light tile A = p, heavy tile B = n_tiles-1-p
-//    (1-D grid, KV head fastest: one head per XCD). Wave w (SIMD w & 3) owns
-//    unit (w & 3) of tile A if w < 4, of tile B otherwise. For short prompts
-//    (fewer tile pairs x KV heads than CUs) a unit is 16 tokens x 1 head and
-//    two workgroups split the 4 query heads of a (KV head, pair); for shorter
-//    ones four 4-wave workgroups (one query head each, wave w on unit w & 1 of
-//    tile A if w < 2, of tile B otherwise).
+// prefill_kernel, a flash-attention over LDS tiles of the image:
+//  * Query tokens form tiles of 32; a "unit" is 16 tokens x 1 GQA head (one
+//    wave's MFMA columns). A workgroup owns one KV head and a zig-zag PAIR of
+//    tiles: light tile A = p, heavy tile B = n_tiles-1-p (grid KV head
+//    fastest: one head per XCD). Two 8-wave workgroups split the 4 query
+//    heads of a (KV head, pair), or four 4-wave workgroups (one query head
+//    each, wave w on unit w & 1 of tile A if w < 2, of tile B otherwise).
 //  * Work balance (split-K inside the workgroup): with n_A / n_B the 64-row
 //    chunks tiles A / B attend and mid = ceil((n_A + n_B) / 2), the B waves
 //    take B's chunks [0, mid) while the A waves take A's chunks [0, n_A) and
@@ -510,7 +515,6 @@ __global__ __launch_bounds__(kPrepThreads, 4) void prefill_prep_kernel(PrefillAr
 }
 
 // Layouts (kHpw query heads per wave, kWaves waves per workgroup):
-//  <2, 8>: a workgroup covers all 4 heads of its KV head;
 //  <1, 8>: short prompts: two workgroups (head sets) share a (KV head, tile
 //      pair) and every wave does half the work, so that twice the workgroups run;
 //  <1, 4>: shorter prompts: four workgroups of 4 waves (one query head each)
@@ -519,7 +523,7 @@ template <int kHpw, int kWaves>
 __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(PrefillArgs a) {
     constexpr int kHeadsPerWave = kHpw;
     constexpr int kUnits = kWaves / 2;     // units per tile: (token half, head group)
-    static_assert((kWaves == 8 && (kHpw == 1 || kHpw == 2)) || (kWaves == 4 && kHpw == 1), "layout");
+    static_assert(kHpw == 1 && (kWaves == 8 || kWaves == 4), "layout");
     // lds[stream][buf]: staged chunk (K rows, V^T rows, K residual rows), 2
     // streams x 2 buffers (160 KB, all of the CU's LDS).
     __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBufHalves];
@@ -1643,10 +1647,8 @@ static void launch_attention(const PrefillArgs& a, uint32_t n_kv_head, hipStream
     if (a.direct) {
         hipLaunchKernelGGL(prefill_split_kernel, dim3(n_kv_head, a.n_ksplit, n_pairs), dim3(512), 0, s, a);
         launch_prefill_merge(a, n_kv_head, s);
-    } else if (a.heads_per_wave == 2 && a.vt_order != 0)
+    } else if (a.heads_per_wave == 2)
         hipLaunchKernelGGL(prefill32_kernel, dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
-    else if (a.heads_per_wave == 2)
-        hipLaunchKernelGGL((prefill_kernel<2, 8>), dim3(n_kv_head, 1, n_pairs), dim3(512), 0, s, a);
     else if (a.wg_waves == 4)
         hipLaunchKernelGGL((prefill_kernel<1, 4>), dim3(n_kv_head, 4, n_pairs), dim3(256), 0, s, a);
     else

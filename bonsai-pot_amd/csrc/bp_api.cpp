@@ -49,7 +49,6 @@ struct bp_model {
     uint32_t prefill_hpw;   // 0 = by grid size, else 1 or 2 query heads per prefill wave
     uint32_t prefill_waves; // 0 = by grid size, else 4 or 8 waves per workgroup at 1 head per wave
     uint32_t prefill_ksplit;   // 0 = by grid size, else the key split count of the 4-wave layout
-    uint32_t prefill_mfma32;   // two-heads layout on prefill32_kernel (1, default) or prefill_kernel<2, 8> (0)
     int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 (default) f16 sums in the reference's order, 2 i8 MFMA
     uint32_t matvec_stream_min_tiles;
     bool lost;
@@ -280,8 +279,6 @@ bp_status bp_model_create(const bp_config* cfg, uint32_t max_seq, int device, bp
         const long v = std::strtol(env, nullptr, 10);
         if (v >= 1 && v <= 64) m->prefill_ksplit = static_cast<uint32_t>(v);
     }
-    m->prefill_mfma32 = 1;
-    if (const char* env = std::getenv("BP_PREFILL_MFMA32")) m->prefill_mfma32 = std::strtol(env, nullptr, 10) != 0;
     m->prefill_waves = 0;
     if (const char* env = std::getenv("BP_PREFILL_WG_WAVES")) {
         const long v = std::strtol(env, nullptr, 10);
@@ -574,7 +571,7 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
     }
     // The 32x32 kernel serves the two-heads layout; its V^T image keys are in
     // its own MFMA order.
-    a.vt_order = a.heads_per_wave == 2 && m->prefill_mfma32 ? 1u : 0u;
+    a.vt_order = a.heads_per_wave == 2 ? 1u : 0u;
     a.scale = 1.0f / std::sqrt(static_cast<float>(m->cfg.head_dim));   // src/forward.rs:524
     a.ws_chunks = (m->max_seq + 63) / 64;
     const uint64_t image_elems = static_cast<uint64_t>(m->cfg.n_kv_head) * a.ws_chunks * 64 * 128;

@@ -89,7 +89,7 @@ struct PrefillArgs {
     uint32_t pos;             // first query's RoPE/cache position when causal
     uint32_t causal;          // 1: token m sees rows [0, pos+m]; 0: rows [0, pos)
     uint32_t n_tiles;         // ceil(m_tokens / kPrefillTileTok)
-    uint32_t heads_per_wave;  // prefill_kernel layout: 2, or 1 (two or four workgroups per tile pair)
+    uint32_t heads_per_wave;  // 2: prefill32_kernel (4 heads x 32 tokens per role); 1: prefill_kernel (two or four workgroups per tile pair)
     uint32_t wg_waves;        // with 1 head per wave: 8 (two head sets) or 4 (four, one head each)
     // Key split (short chunks over long caches, with direct = 1): n_ksplit > 1
     // workgroups of prefill_split_kernel per (KV head, tile pair), each over

@@ -1077,14 +1077,6 @@ __global__ __launch_bounds__(512) void prefill32_kernel(PrefillArgs a) {
             lds_copy(ls + 16 * piece, reinterpret_cast<uint8_t*>(dst + kKHalves) + 16 * piece);
         }
     };
-    auto copy_v4 = [&](uint16_t* dst, uint32_t ch) __attribute__((always_inline)) {
-        const uint16_t* vs = vt16 + static_cast<uint64_t>(ch) * kVHalves;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int piece = 64 * (4 * r + rw);
-            lds_copy(vs + 8 * piece, dst + 8 * piece);
-        }
-    };
 
     // ---- MFMA phase pieces --------------------------------------------------
     // Both MFMA blocks keep four LDS fragment reads in flight ahead of the

@@ -940,8 +940,7 @@ bp_status bp_attention_decode_noalloc(const bp_config* cfg, void* kv_k, void* kv
     if (static_cast<uint64_t>(a.n_splits) * cfg->n_head * bp::decode_partial_stride() > kNoAllocScratchFloats)
         return fail(BP_ERR_CONFIG, "noalloc decode: %u query heads x %u splits exceed the %llu-float scratch",
                     cfg->n_head, a.n_splits, static_cast<unsigned long long>(kNoAllocScratchFloats));
-    bp::launch_decode(a, cfg->n_kv_head, static_cast<hipStream_t>(stream));
-    e = hipGetLastError();
+    e = bp::launch_decode(a, cfg->n_kv_head, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(BP_ERR_HIP, "attention_decode_noalloc launch: %s", hipGetErrorString(e));
     return BP_OK;
 }

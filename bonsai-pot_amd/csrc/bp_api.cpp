@@ -539,11 +539,11 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
         a.wg_waves = 8;
         if (a.heads_per_wave == 1)
             a.wg_waves = m->prefill_waves != 0 ? m->prefill_waves : (4 * pairs * m->cfg.n_kv_head <= cus ? 4u : 8u);
-        // Key split for short chunks over long caches (4-wave layout): while
-        // one workgroup per (tile, KV head, query head) leaves most CUs idle,
-        // split every tile's key range over n_ksplit workgroups of at least 8
-        // chunks each (fewer splits when the partials would not fit), then
-        // merge. BP_PREFILL_KSPLIT forces a split count (within the partials).
+        // Key split for short chunks over long caches (where the 4-wave
+        // layout would be chosen): split every tile pair's key range over
+        // n_ksplit workgroups (fewer splits when the partials would not fit),
+        // then merge. BP_PREFILL_KSPLIT forces a split count (within the
+        // partials).
         a.n_ksplit = 1;
         a.split_chunks = 0;
         a.kpart = m->partials;

@@ -46,7 +46,7 @@ struct bp_model {
     uint16_t* q_norm;     // decode-step scratch: normalized q, [n_head][128] f16
     uint32_t decode_min_split_rows;
     uint32_t decode_wide_min_rows;
-    uint32_t prefill_hpw;   // 0 = by grid size, else 1 or 2 query heads per prefill wave
+    uint32_t prefill_hpw;   // 0 = by grid size; 2 = prefill32_kernel, 1 = the one-head 16x16 kernels
     uint32_t prefill_waves; // 0 = by grid size, else 4 or 8 waves per workgroup at 1 head per wave
     uint32_t prefill_ksplit;   // 0 = by grid size, else the key split count of the 4-wave layout
     int matvec_arith;        // Q1_0 matvecs: 0 auto, 1 (default) f16 sums in the reference's order, 2 i8 MFMA
@@ -527,12 +527,13 @@ static bp_status prefill_args(bp_model* m, void* act, uint32_t q_off, uint32_t o
     a.causal = is_prefill ? 1u : 0u;
     a.n_tiles = (m_tokens + bp::kPrefillTileTok - 1) / bp::kPrefillTileTok;
     {
-        // One query head per wave (twice the workgroups, half the work each) while
-        // that grid still fits the compute units at one workgroup each; measured
-        // at 128-1024 tokens 1.3-1.4x faster, at 1536 (384 workgroups) 1.25x
-        // slower. Then 4-wave workgroups (four times the workgroups of the
-        // two-heads layout) while those fit. BP_PREFILL_HEADS_PER_WAVE and
-        // BP_PREFILL_WG_WAVES force a layout.
+        // The one-head 16x16 kernels (two 8-wave workgroups per tile pair and KV
+        // head, each wave 16 tokens of one query head) while that grid still
+        // fits the compute units at one workgroup each, else prefill32_kernel
+        // (one 8-wave workgroup per tile pair and KV head; at 64-1024 tokens it
+        // measured 12.0-32.5 us against 10.1-27.3 us for the 16x16 kernels).
+        // Then 4-wave workgroups (four per tile pair and KV head) while those
+        // fit. BP_PREFILL_HEADS_PER_WAVE and BP_PREFILL_WG_WAVES force a layout.
         const uint32_t pairs = (a.n_tiles + 1) / 2;
         const uint32_t cus = static_cast<uint32_t>(m->cu_count > 0 ? m->cu_count : 256);
         a.heads_per_wave = m->prefill_hpw != 0 ? m->prefill_hpw : (2 * pairs * m->cfg.n_kv_head <= cus ? 1u : 2u);

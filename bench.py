@@ -274,14 +274,43 @@ def bench_prefill(torch, args, m, pos):
         b.model.dispatch_kv_writeback_fused(b.a, b.wp, b.k_off, b.v_off, b.cfg.head_dim, i % n_layer, pos, m)
         b.model.dispatch_attention(b.a, b.q_off, b.out_off, i % n_layer, pos, m, True)
     unfused_us = per_launch_us(torch, b, _unfused, n)
+    mfma_tf = bench_mfma_rate(torch, b) if m == 2048 and pos == 0 else None
     b.model.close()
-    return {"m_tokens": m, "pos_base": pos, "flops": flops, "kernel_us_avg": avg_us,
+    extra = {}
+    if mfma_tf is not None:
+        extra = {"mfma_sustained_random_TFLOPs": mfma_tf,
+                 "frac_of_sustained_mfma": tflops / mfma_tf,
+                 "step_attention_frac_of_sustained_mfma": flops / ((step_us - prep_us) * 1e-6) / 1e12 / mfma_tf}
+    return {**extra, "m_tokens": m, "pos_base": pos, "flops": flops, "kernel_us_avg": avg_us,
             "TFLOPs": tflops, "frac_f16_mfma": tflops / F16_MFMA_PEAK_TFLOPS,
             "q_norm_rope_us": qn_us, "kv_writeback_us": wb_us,
             "kv_writeback_GBps": m * 8 * (2 * 256 + 2 * 144) / (wb_us * 1e-6) / 1e9,
             "step_us": step_us, "step_prep_us": prep_us, "step_unfused_us": unfused_us,
             "step_attention_us": step_us - prep_us,
             "step_attention_frac_f16_mfma": flops / ((step_us - prep_us) * 1e-6) / 1e12 / F16_MFMA_PEAK_TFLOPS}
+
+
+def bench_mfma_rate(torch, b):
+    """The f16 matrix rate this GPU sustains on real data (TFLOP/s): the bench
+    library's bp_debug_mfma_rate (back-to-back v_mfma_f32_32x32x16_f16 on random
+    f16 operands, one 4-wave workgroup per CU, 16384 x 4 MFMAs per wave) per
+    launch in a graph after the warm-up. Random operands draw more power than
+    constant ones, and the clock drops accordingly; this is the ceiling a
+    prefill on real data can approach, beside the 2.5 PFLOP/s nominal peak
+    that frac_f16_mfma is priced against."""
+    from bonsai_pot_amd import lib as _lib
+    n_wg = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 16384
+    sink = torch.zeros(n_wg * 256, device="cuda", dtype=torch.float32)
+
+    class _R:
+        model = b.model
+
+    def _run(i):
+        rc = _lib.bp_debug_mfma_rate(sink.data_ptr(), iters, n_wg, i + 1, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    us = per_launch_us(torch, _R, _run, 4)
+    return n_wg * 4 * iters * 4 * 32768 / (us * 1e-6) / 1e12
 
 
 def bench_copy(torch, args, nbytes=1 << 30):

@@ -96,6 +96,7 @@ _SIGS = {
 _BENCH_SIGS = {
     "bp_debug_prefill_prep": (_i32, [_vp, _vp, _vp] + [_u32] * 9),
     "bp_debug_read_floor": (_i32, [_vp, _u64, _vp, _u32, _vp]),
+    "bp_debug_mfma_rate": (_i32, [_vp, _u32, _u32, _u32, _vp]),
 }
 EXPORTED_SYMBOLS = tuple(_SIGS)
 BENCH_SYMBOLS = tuple(_BENCH_SIGS)

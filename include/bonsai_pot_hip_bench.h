@@ -20,6 +20,14 @@ extern "C" {
  * byte count. */
 bp_status bp_debug_read_floor(const void* src, uint64_t bytes, void* sink, uint32_t n_workgroups, void* stream);
 
+/* Measurement aid, no counterpart in the reference and not part of the
+ * attention path: `iters` x 4 back-to-back v_mfma_f32_32x32x16_f16 per wave
+ * on random f16 operands, `n_workgroups` workgroups of 4 waves, on `stream`;
+ * writes one float per thread to `sink` (n_workgroups x 1 KB). That is
+ * n_workgroups x 4 x iters x 4 x 32768 flops; bench.py times it as the f16
+ * matrix rate the GPU sustains on real (random) data. */
+bp_status bp_debug_mfma_rate(void* sink, uint32_t iters, uint32_t n_workgroups, uint32_t seed, void* stream);
+
 /* Measurement aid, no counterpart in the reference: the first of the two
  * launches of bp_dispatch_attention_prefill_step alone (q norm + RoPE, the
  * K/V writeback and the attention kernel's f16 image of the layer's rows),

@@ -175,11 +175,13 @@ def test_attention_non_causal_multi_token(cuda):
     assert_attn_close(dev.out_f32(), want, "non-causal")
 
 
-@pytest.mark.parametrize("m,pos_base", [(2048, 0), (2048, 2048)])
+@pytest.mark.parametrize("m,pos_base", [(2048, 0), (2048, 2048), (64, 16384)])
 def test_prefill_full_size_sampled_rows(cuda, m, pos_base):
-    """pp2048 (metric) and config 4 (2048-token chunk over a 2048-row cache):
-    the whole output is computed on the GPU, the oracle checks sampled tokens
-    spread over every 64-token tile, including first/last rows."""
+    """pp2048 (metric), config 4 (2048-token chunk over a 2048-row cache) and
+    the bench's chat-turn shape (64 tokens over 16384 rows: the key-split
+    kernel at its default 32 splits): the whole output is computed on the
+    GPU, the oracle checks sampled tokens spread over every 64-token tile,
+    including first/last rows."""
     _say(f"[prefill-full] m={m} pos_base={pos_base}")
     cfg = layout.Config(n_layer=1)
     sc = Scenario(cfg, max_seq=pos_base + m, m_tokens=m, seed=m + pos_base)
@@ -191,6 +193,7 @@ def test_prefill_full_size_sampled_rows(cuda, m, pos_base):
     rng = np.random.default_rng(1)
     tokens = np.unique(np.concatenate([[0, 1, 15, 16, 63, 64, m - 1],
                                        np.arange(0, m, 64) + rng.integers(0, 64, m // 64)]))
+    tokens = tokens[tokens < m] if m > 128 else np.arange(m)   # short chunks: every token
     want = sc.oracle_attention(0, pos_base, is_prefill=True, tokens=tokens)
     got = dev.out_f32()[tokens]
     assert_attn_close(got, want, f"prefill m={m} pos_base={pos_base}")

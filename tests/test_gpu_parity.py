@@ -109,6 +109,28 @@ def test_decode_vs_oracle(cuda, monkeypatch, pos, layout_name):
     assert_attn_close(dev.out_f32(1)[0], want, f"decode pos={pos}")
 
 
+@pytest.mark.parametrize("pos", [65536, 99999])
+def test_decode_long_context(cuda, pos):
+    """Past 128 x 256 rows the split plan keeps 128 splits and lengthens them
+    (65536: 512 rows each, 16 batches per wave; 99999: 800 rows, an odd 25
+    batches per wave and a short last split): the plain decode and the fused
+    step against the oracle."""
+    _say(f"[decode] long context pos={pos}")
+    cfg = layout.Config(n_layer=1)
+    sc = Scenario(cfg, max_seq=pos + 1, m_tokens=1, seed=300 + pos % 1000)
+    _prefill_cache(sc, 0, pos, seed=400 + pos % 1000)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.decode_step(0, pos)
+    sc.oracle_q_norm_rope(pos)
+    sc.oracle_writeback(0, pos)
+    k, v = dev.kv_host()
+    assert np.array_equal(k, sc.kv_k) and np.array_equal(v, sc.kv_v), "cache bytes differ"
+    _, want = sc.oracle_decode(0, pos)
+    assert_attn_close(dev.out_f32(1)[0], want, f"decode step pos={pos}")
+    dev.decode(0, pos)   # plain entry point on the normalized q the step left in act
+    assert_attn_close(dev.out_f32(1)[0], want, f"decode pos={pos}")
+
+
 def test_decode_ctx32k_with_outlier_rows(cuda):
     """Config 5: ctx 32768 (32769 rows), 1% of key rows x8 before quantization
     (x8 = a w_k_norm of 8.0 for those rows, exact in f16)."""

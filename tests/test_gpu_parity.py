@@ -221,6 +221,28 @@ def test_prefill_full_size_sampled_rows(cuda, m, pos_base):
     assert_attn_close(got, want, f"prefill m={m} pos_base={pos_base}")
 
 
+@pytest.mark.parametrize("m,pos_base", [(100, 30000), (1000, 8000), (2048, 6000)])
+def test_prefill_long_cache_sampled_rows(cuda, m, pos_base):
+    """Chunks over long caches in each layout the library picks by default:
+    100 tokens on 30000 rows (the key split), 1000 on 8000 (the one-head
+    8-wave kernel over the image) and 2048 on 6000 (prefill32_kernel); the
+    oracle checks sampled tokens of every 64-token tile, first and last
+    included."""
+    _say(f"[prefill-long] m={m} pos_base={pos_base}")
+    cfg = layout.Config(n_layer=1)
+    sc = Scenario(cfg, max_seq=pos_base + m, m_tokens=m, seed=m + pos_base)
+    _prefill_cache(sc, 0, pos_base, seed=78)
+    sc.oracle_q_norm_rope(pos_base)
+    sc.oracle_writeback(0, pos_base)
+    dev = DeviceScenario(sc, upload_kv=True)
+    dev.attention(0, pos_base, is_prefill=True)
+    rng = np.random.default_rng(2)
+    tokens = np.unique(np.concatenate([[0, 1, 31, 32, m - 1], np.arange(0, m, 64) + rng.integers(0, 64, (m + 63) // 64)]))
+    tokens = tokens[tokens < m]
+    want = sc.oracle_attention(0, pos_base, is_prefill=True, tokens=tokens)
+    assert_attn_close(dev.out_f32()[tokens], want, f"prefill m={m} pos_base={pos_base}")
+
+
 def test_decode_repeated_calls_fresh_partials(cuda):
     """Back-to-back decodes on one model (different layers, positions and queries)
     reuse the split-K scratch and tickets; every output must match its own oracle
